@@ -1,0 +1,134 @@
+/*
+ * kotflash_amd C ABI: the drop-in boundary of the attention hot path.
+ *
+ * One shared library (kotflash_amd/libkotflash_amd.so, gfx950 code objects)
+ * exports these entry points. They replace the reference's host launcher layer
+ * (the Python functions that allocate outputs and launch Triton kernels) and its
+ * pybind11 K/V append op. Conventions, kept from the reference launchers:
+ *
+ *  - every tensor pointer is a device pointer owned by the caller (torch);
+ *    inputs are borrowed, outputs and workspaces are caller-allocated;
+ *  - tensors are [batch, heads, sequence, head_dim] with a unit head_dim
+ *    stride; the other three strides are given in elements, as int64_t[3]
+ *    {batch, head, sequence}; 16-byte aligned base pointers and strides that are
+ *    multiples of 8 elements are required (KF_EINVAL otherwise);
+ *  - head_dim D is a multiple of 8 in [8, 128]; the GQA map is
+ *    kv_head = q_head / (Hq / Hkv) (contiguous groups, repeat_interleave);
+ *  - causal masking is upper-left: key j is visible to query i iff j <= i;
+ *  - LSE is the natural-log row log-sum-exp in fp32, contiguous [B, Hq, Sq];
+ *  - launches are asynchronous on the given HIP stream of the current device;
+ *    nothing here allocates device memory, synchronizes or is thread-safe
+ *    with respect to concurrent use of the same output buffers;
+ *  - the return value is KF_OK (0) or a KF_E* code; kf_last_error() then
+ *    holds a message for the calling thread.
+ */
+#ifndef KOTFLASH_AMD_H_
+#define KOTFLASH_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KF_ABI_VERSION 1
+
+enum kf_status {
+  KF_OK = 0,
+  KF_EINVAL = 1,       /* invalid argument (shape, stride, alignment, pointer) */
+  KF_EUNSUPPORTED = 2, /* valid but outside what the kernels implement */
+  KF_ELAUNCH = 3       /* HIP reported a launch failure */
+};
+
+enum kf_dtype { KF_F16 = 0, KF_BF16 = 1 };
+
+/* Message for the last failing call on this thread. */
+const char* kf_last_error(void);
+/* KF_ABI_VERSION of the loaded library. */
+int kf_abi_version(void);
+
+/*
+ * Attention forward: O = softmax(scale * Q K^T + mask) V and its LSE.
+ * Replaces attention_forward + _attention_fwd_kernel
+ * (reference kotflash/kernels/triton_forward.py:372-456 and :20-165).
+ * o has q's shape; lse is fp32 contiguous [B, Hq, Sq].
+ */
+int kf_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                const int64_t* o_strides, float scale, int causal, int dtype, void* stream);
+
+/*
+ * Workspace for kf_attn_bwd in bytes (fp32 row deltas and partial sums).
+ */
+size_t kf_attn_bwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk,
+                                   int64_t D, int causal);
+
+/*
+ * Attention backward: dQ, dK, dV from Q, K, V, O, LSE and dO. dK/dV are summed
+ * over the Hq/Hkv query heads of each KV group. The row delta
+ * rowsum(O * dO) is computed from the stored low-precision O.
+ * Replaces attention_backward + _attention_bwd_dq/_dkv/_dkv_split/_dkv_reduce
+ * (reference kotflash/kernels/triton_backward.py:335-421, :17-332).
+ * dq/dk/dv have q/k/v's shapes; strides are int64_t[3] like the inputs.
+ */
+int kf_attn_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                const void* dout, void* dq, void* dk, void* dv, int64_t B, int64_t Hq,
+                int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D, const int64_t* q_strides,
+                const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+                const int64_t* do_strides, const int64_t* dq_strides, const int64_t* dk_strides,
+                const int64_t* dv_strides, float scale, int causal, int dtype, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/*
+ * Number of KV splits the gfx950 decode planner picks for a short-query,
+ * long-cache problem (keys per split are a multiple of 64).
+ */
+int kf_decode_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D);
+
+/* Workspace for kf_attn_decode in bytes (fp32 partial O and LSE per split). */
+size_t kf_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Sq, int64_t D, int num_splits);
+
+/*
+ * Split-KV decode, non-causal: every query row sees keys [0, L_b) of its
+ * batch entry, L_b = seqlens_k[b] (device int32, nullable: L_b = Sk for all b).
+ * K/V may be strided prefix views of a larger cache (sequence stride >= D).
+ * Each workgroup reads one KV chunk of one (batch, kv_head) once for all
+ * Hq/Hkv * Sq query rows; a second kernel merges the per-split (O, LSE)
+ * partials with LSE weights. lse is nullable.
+ * Replaces attention_forward_strided_decode + _strided_decode_split /
+ * _strided_decode_reduce (reference kotflash/kernels/triton_decode.py:412-468,
+ * :16-104, :241-297) and the split-KV branch of attention_forward
+ * (triton_forward.py:410-445, kernels :169-349).
+ */
+int kf_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse,
+                   const int32_t* seqlens_k, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
+                   int64_t Sk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides, const int64_t* o_strides, float scale,
+                   int num_splits, int dtype, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/*
+ * K/V cache append: cache[b, h, start_b + t, :] = new[b, h, t, :] for K and V
+ * in one launch, bit-exact. start_b = start_dev[b] when start_dev (device
+ * int64 [B]) is non-null, else the scalar start. Rows that would land at or
+ * beyond `capacity` are not written (callers validate first; the reference
+ * rejects such appends before launching). new_k/new_v may have any strides
+ * (int64_t[4], element units, including head_dim); the caches need a unit
+ * head_dim stride.
+ * Replaces append_kv_cuda / append_kv_ (reference
+ * kotflash/csrc/kv_append_cuda.cu:12-96, kotflash/csrc/kv_append.cpp:11-14),
+ * extended from one scalar start to per-sequence positions.
+ */
+int kf_kv_append(void* k_cache, void* v_cache, const void* new_k, const void* new_v,
+                 const int64_t* start_dev, int64_t start, int64_t B, int64_t H, int64_t Snew,
+                 int64_t D, int64_t capacity, const int64_t* k_cache_strides,
+                 const int64_t* v_cache_strides, const int64_t* new_k_strides4,
+                 const int64_t* new_v_strides4, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KOTFLASH_AMD_H_ */

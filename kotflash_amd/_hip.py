@@ -1,0 +1,196 @@
+"""ctypes binding of ``libkotflash_amd.so``, the C ABI declared in
+``include/kotflash_amd.h``.
+
+This module is the host launcher layer of the reference (the functions that
+allocate outputs with torch and launch kernels on the current stream; reference
+kotflash/kernels/triton_forward.py:372-456, triton_backward.py:335-421,
+triton_decode.py:302-468, kotflash/_cuda_append.py:31-44). Tensors stay torch
+tensors; only raw device pointers, sizes, strides and the HIP stream of
+PyTorch's current stream cross the boundary. There is no CPU fallback here: if
+the library is missing or a call fails, a RuntimeError is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+from functools import lru_cache
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libkotflash_amd.so"
+ABI_VERSION = 1
+KF_F16, KF_BF16 = 0, 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+_I64P = ctypes.POINTER(ctypes.c_int64)
+
+_SIGNATURES = {
+    "kf_last_error": (ctypes.c_char_p, []),
+    "kf_abi_version": (_I, []),
+    "kf_attn_fwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                         _I64P, _I64P, _I64P, _I64P, _F, _I, _I, _P]),
+    "kf_attn_bwd_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I]),
+    "kf_attn_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                         _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P,
+                         _F, _I, _I, _P, _SZ, _P]),
+    "kf_decode_num_splits": (_I, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "kf_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
+    "kf_attn_decode": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                            _I64P, _I64P, _I64P, _I64P, _F, _I, _I, _P, _SZ, _P]),
+    "kf_kv_append": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                          _I64P, _I64P, _I64P, _I64P, _I, _P]),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+
+@lru_cache(maxsize=1)
+def lib() -> ctypes.CDLL:
+    """Load the library (after torch, so it binds to torch's HIP runtime)."""
+    if not LIB_PATH.is_file():
+        raise RuntimeError(
+            f"kotflash_amd HIP library not found at {LIB_PATH}; "
+            "build it with `python -m kotflash_amd.build`"
+        )
+    handle = ctypes.CDLL(str(LIB_PATH))
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = handle.kf_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"kotflash_amd ABI mismatch: library {version}, bindings {ABI_VERSION}")
+    return handle
+
+
+def library_available() -> bool:
+    try:
+        lib()
+    except (OSError, RuntimeError):
+        return False
+    return True
+
+
+@lru_cache(maxsize=16)
+def device_arch(index: int) -> str:
+    return torch.cuda.get_device_properties(index).gcnArchName.split(":")[0]
+
+
+def is_gfx950(device: torch.device) -> bool:
+    if device.type != "cuda" or not torch.cuda.is_available():
+        return False
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return device_arch(index) == "gfx950"
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float16:
+        return KF_F16
+    if dtype == torch.bfloat16:
+        return KF_BF16
+    raise TypeError(f"HIP kernels support float16 and bfloat16, got {dtype}")
+
+
+def _strides(t: torch.Tensor, n: int = 3):
+    arr = (ctypes.c_int64 * 4)(*t.stride())
+    return ctypes.cast(arr, _I64P), arr  # keep arr alive with the pointer
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().kf_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def layout_ok(t: torch.Tensor) -> bool:
+    """Whether the kernels can read ``t`` in place: unit head_dim stride,
+    other strides multiples of 8 elements, 16-byte aligned base."""
+    if t.ndim != 4 or t.stride(3) != 1:
+        return False
+    if any(s % 8 for s in t.stride()[:3]):
+        return False
+    return t.data_ptr() % 16 == 0
+
+
+def fwd(q, k, v, out, lse, *, causal: bool, scale: float) -> None:
+    b, hq, sq, d = q.shape
+    _, hkv, sk, _ = k.shape
+    keep = [_strides(t) for t in (q, k, v, out)]
+    with torch.cuda.device(q.device):
+        rc = lib().kf_attn_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+            b, hq, hkv, sq, sk, d, *(s[0] for s in keep),
+            float(scale), int(bool(causal)), dtype_code(q.dtype), _stream(q.device),
+        )
+    _check(rc, "kf_attn_fwd")
+
+
+def bwd_workspace_bytes(b, hq, hkv, sq, sk, d, causal) -> int:
+    return int(lib().kf_attn_bwd_workspace_bytes(b, hq, hkv, sq, sk, d, int(bool(causal))))
+
+
+def bwd(q, k, v, out, lse, dout, dq, dk, dv, *, causal: bool, scale: float,
+        workspace: torch.Tensor) -> None:
+    b, hq, sq, d = q.shape
+    _, hkv, sk, _ = k.shape
+    keep = [_strides(t) for t in (q, k, v, out, dout, dq, dk, dv)]
+    with torch.cuda.device(q.device):
+        rc = lib().kf_attn_bwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+            dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+            b, hq, hkv, sq, sk, d, *(s[0] for s in keep),
+            float(scale), int(bool(causal)), dtype_code(q.dtype),
+            workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+            _stream(q.device),
+        )
+    _check(rc, "kf_attn_bwd")
+
+
+def decode_num_splits(b, hq, hkv, sq, sk, d) -> int:
+    return int(lib().kf_decode_num_splits(b, hq, hkv, sq, sk, d))
+
+
+def decode_workspace_bytes(b, hq, sq, d, num_splits) -> int:
+    return int(lib().kf_decode_workspace_bytes(b, hq, sq, d, num_splits))
+
+
+def decode(q, k, v, out, lse: Optional[torch.Tensor], seqlens: Optional[torch.Tensor], *,
+           scale: float, num_splits: int, workspace: Optional[torch.Tensor]) -> None:
+    b, hq, sq, d = q.shape
+    _, hkv, sk, _ = k.shape
+    keep = [_strides(t) for t in (q, k, v, out)]
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    with torch.cuda.device(q.device):
+        rc = lib().kf_attn_decode(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            lse.data_ptr() if lse is not None else None,
+            seqlens.data_ptr() if seqlens is not None else None,
+            b, hq, hkv, sq, sk, d, *(s[0] for s in keep),
+            float(scale), int(num_splits), dtype_code(q.dtype), ws_ptr, ws_bytes,
+            _stream(q.device),
+        )
+    _check(rc, "kf_attn_decode")
+
+
+def kv_append(k_cache, v_cache, new_k, new_v, *, start: int = 0,
+              start_dev: Optional[torch.Tensor] = None) -> None:
+    b, h, s, d = new_k.shape
+    keep = [_strides(t) for t in (k_cache, v_cache, new_k, new_v)]
+    with torch.cuda.device(k_cache.device):
+        rc = lib().kf_kv_append(
+            k_cache.data_ptr(), v_cache.data_ptr(), new_k.data_ptr(), new_v.data_ptr(),
+            start_dev.data_ptr() if start_dev is not None else None, int(start),
+            b, h, s, d, k_cache.shape[2], *(x[0] for x in keep),
+            dtype_code(k_cache.dtype), _stream(k_cache.device),
+        )
+    _check(rc, "kf_kv_append")

@@ -1,0 +1,57 @@
+"""One-launch K/V cache append on gfx950.
+
+Counterpart of the reference's optional CUDA op (kotflash/_cuda_append.py:31-44
+and kotflash/csrc/kv_append_cuda.cu:50-75): same argument checks, same
+exceptions, but the library is built ahead of time (no JIT), fp16 and bf16 are
+accepted, and ``start`` may be a per-sequence device tensor.
+"""
+from __future__ import annotations
+
+from typing import Union
+
+import torch
+
+from . import _hip
+
+
+def append_kv_hip(k_cache, v_cache, new_k, new_v, start: Union[int, torch.Tensor]) -> None:
+    """Write new_k/new_v [B, H, S, D] into the caches [B, H, capacity, D] at
+    positions start .. start+S-1 (``start`` an int, or a device int64 [B]
+    tensor of per-sequence positions)."""
+    if not torch.cuda.is_available():
+        raise RuntimeError("a GPU is required for the kotflash_amd append kernel")
+    tensors = (k_cache, v_cache, new_k, new_v)
+    if any(not t.is_cuda for t in tensors):
+        raise ValueError("all cache and source tensors must be GPU tensors")
+    if any(t.dtype not in (torch.float16, torch.bfloat16) for t in tensors):
+        raise TypeError("the HIP append kernel supports FP16 and BF16 only")
+    if any(t.dtype != k_cache.dtype for t in tensors):
+        raise TypeError("all cache and source tensors must share one dtype")
+    if any(t.device != k_cache.device for t in tensors):
+        raise ValueError("all cache and source tensors must be on the same GPU")
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise RuntimeError("K/V cache must have matching [B,H,capacity,D] shapes")
+    if new_k.dim() != 4 or new_v.shape != new_k.shape:
+        raise RuntimeError("new K/V must have matching [B,H,S,D] shapes")
+    if k_cache.stride(3) != 1 or v_cache.stride(3) != 1:
+        raise RuntimeError("destination K/V caches need a unit head_dim stride")
+    if (new_k.shape[0] != k_cache.shape[0] or new_k.shape[1] != k_cache.shape[1]
+            or new_k.shape[3] != k_cache.shape[3]):
+        raise RuntimeError("new K/V batch, heads and head_dim must match the cache")
+    if new_k.shape[2] <= 0 or new_k.shape[3] <= 0:
+        raise RuntimeError("new K/V dimensions must be non-empty")
+    if not _hip.is_gfx950(k_cache.device):
+        raise RuntimeError("the HIP append kernel requires an AMD gfx950 (MI355X) device")
+    if isinstance(start, torch.Tensor):
+        if start.dtype != torch.int64 or start.device != k_cache.device or start.shape != (new_k.shape[0],):
+            raise ValueError("per-sequence start must be a device int64 tensor of shape [B]")
+        _hip.kv_append(k_cache, v_cache, new_k, new_v, start_dev=start)
+    else:
+        start = int(start)
+        if start < 0 or start + new_k.shape[2] > k_cache.shape[2]:
+            raise RuntimeError("append range exceeds cache capacity")
+        _hip.kv_append(k_cache, v_cache, new_k, new_v, start=start)
+
+
+# Name kept for drop-in callers of the reference's op.
+append_kv_cuda = append_kv_hip

@@ -1,0 +1,354 @@
+// Attention forward for gfx950: online softmax with MFMA QK^T and PV.
+//
+// Work decomposition. One workgroup (4 waves) owns BM = 4 * QB * 32 query rows
+// of one (batch, q_head). Each wave owns QB blocks of 32 rows and keeps them
+// for the whole kernel:
+//   - Q rows in registers as MFMA B operands,
+//   - the running max m, the running denominator l and the output accumulator
+//     O^T (head_dim x rows) in registers.
+// The workgroup streams K/V in tiles of BN = 64 keys through LDS (register
+// prefetch of tile n+1 overlaps the MFMAs of tile n; LDS is double-buffered so
+// one barrier per tile suffices).
+//
+// Per tile and 32-row block the wave computes S^T = K Q^T (keys x rows), so a
+// lane owns one query row and 32 of the tile's 64 scores in registers: the row
+// max/sum are in-lane reductions plus one exchange with lane^32. P^T is then
+// already laid out as the B operand of O^T += V^T P^T, and V^T is read from the
+// row-major V tile with ds_read_b64_tr_b16.
+//
+// Semantics follow the reference forward (kotflash/kernels/triton_forward.py
+// :20-165): scores scaled before masking (:104,:116), mask (i < Sq, j < Sk,
+// causal j <= i) (:118-121), causal tile skip end = min(Sk, Sq, (tile+1) BM)
+// (:69-76), P rounded to the input dtype before the PV product (:131,:135),
+// O stored in the input dtype (:139-158), LSE = m + ln(l) in fp32 (:160-165).
+// exp/log use the hardware base-2 instructions with the scale folded into
+// log2(e).
+#include "kf_common.hpp"
+#include "kf_host.hpp"
+
+namespace kf {
+
+struct FwdParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  float* lse;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int B, Hq, Hkv, Sq, Sk, D;
+  int nqt;
+  float scale_log2;
+};
+
+// Block -> (q tile, batch, q head). Tiles are issued longest first (causal
+// tiles near the end of the sequence see the most keys). When the number of KV
+// groups is a multiple of the 8 XCDs, the workgroups of one KV group are kept
+// on one XCD (the dispatcher assigns block i to XCD i % 8) so its L2 serves the
+// group's K/V to all of them.
+__device__ inline void fwd_map_block(int bid, int nqt, int B, int Hq, int Hkv, int& qt, int& b,
+                                     int& h) {
+  const int G = Hq / Hkv;
+  const int ngroups = B * Hkv;
+  if ((ngroups & 7) == 0) {
+    const int x = bid & 7, j = bid >> 3;
+    const int gpx = ngroups >> 3;
+    const int per_tile = G * gpx;
+    const int t = j / per_tile, r = j - t * per_tile;
+    qt = nqt - 1 - t;
+    const int grp = x + 8 * (r / G);
+    const int g = r % G;
+    b = grp / Hkv;
+    h = (grp % Hkv) * G + g;
+  } else {
+    const int bh = B * Hq;
+    const int t = bid / bh, r = bid - t * bh;
+    qt = nqt - 1 - t;
+    b = r / Hq;
+    h = r % Hq;
+  }
+}
+
+template <typename T, int DT, int QB, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void fwd_kernel(const FwdParams p) {
+  constexpr int BM = 4 * QB * 32;
+  constexpr int BN = 64;
+  constexpr int KSTR = DT + 8;   // 16-byte pad: conflict-free b128 row reads
+  constexpr int VSTR = DT + 16;  // 32-byte pad: conflict-free transposed reads
+  constexpr int KT = BN * KSTR;
+  constexpr int STAGE = KT + BN * VSTR;
+  constexpr int CPR = DT / 8;           // 16-byte chunks per row
+  constexpr int CPT = BN * CPR / 256;   // chunks per thread per tile and matrix
+  constexpr int NKS = DT / 16;          // MFMA k-steps over head_dim
+  constexpr int NDB = DT / 32;          // 32-wide head_dim blocks of O^T
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, h32 = lane >> 5;
+
+  int qt, b, h;
+  fwd_map_block(blockIdx.x, p.nqt, p.B, p.Hq, p.Hkv, qt, b, h);
+  const int kvh = h / (p.Hq / p.Hkv);
+  const int q0 = qt * BM;
+  const int wq0 = q0 + wave * QB * 32;
+
+  const uint16_t* Qp = p.q + b * p.q_sb + h * p.q_sh;
+  const uint16_t* Kp = p.k + b * p.k_sb + kvh * p.k_sh;
+  const uint16_t* Vp = p.v + b * p.v_sb + kvh * p.v_sh;
+
+  u32x4 qf[QB][NKS];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int row = wq0 + qb * 32 + l32;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d = 16 * ks + 8 * h32;
+      qf[qb][ks] = (row < p.Sq && d < p.D) ? ldg16(Qp + row * p.q_ss + d) : zero_u4();
+    }
+  }
+
+  f32x16 oacc[QB][NDB];
+  float m_i[QB], l_i[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_i[qb] = kNegInf;
+    l_i[qb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) oacc[qb][db] = zero16();
+  }
+
+  const int nkeys = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
+  const int ntiles = cdiv(nkeys, BN);
+
+  u32x4 kreg[CPT], vreg[CPT];
+  auto gload = [&](int tile) {
+    const int kbase = tile * BN;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int e = tid + 256 * c;
+      const int row = e / CPR, col = e % CPR;
+      const int key = kbase + row;
+      const bool ok = key < p.Sk && col * 8 < p.D;
+      kreg[c] = ok ? ldg16(Kp + key * p.k_ss + col * 8) : zero_u4();
+      vreg[c] = ok ? ldg16(Vp + key * p.v_ss + col * 8) : zero_u4();
+    }
+  };
+  auto sstore = [&](int buf) {
+    uint16_t* Ks = smem + buf * STAGE;
+    uint16_t* Vs = Ks + KT;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int e = tid + 256 * c;
+      const int row = e / CPR, col = e % CPR;
+      lds_write16(Ks + row * KSTR + col * 8, kreg[c]);
+      lds_write16(Vs + row * VSTR + col * 8, vreg[c]);
+    }
+  };
+
+  if (ntiles > 0) {
+    gload(0);
+    sstore(0);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    if (it + 1 < ntiles) gload(it + 1);
+    const uint16_t* Ks = smem + buf * STAGE;
+    const uint16_t* Vs = Ks + KT;
+    const int kbase = it * BN;
+    // A causal tile whose first key is beyond every row of the wave is fully
+    // masked for it.
+    const bool active = !CAUSAL || kbase <= wq0 + QB * 32 - 1;
+    if (active) {
+      f32x16 s[QB][2];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        s[qb][0] = zero16();
+        s[qb][1] = zero16();
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+          const u32x4 a = lds_read16(Ks + (kb * 32 + l32) * KSTR + 16 * ks + 8 * h32);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) s[qb][kb] = Elem<T>::mfma(a, qf[qb][ks], s[qb][kb]);
+        }
+      }
+
+      const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && kbase + BN - 1 > wq0);
+      u32x4 pk[QB][4];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const int qrow = wq0 + qb * 32 + l32;
+        float mx = kNegInf;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float x = s[qb][kb][r] * p.scale_log2;
+            if (need_mask) {
+              const int key = kbase + 32 * kb + 8 * (r >> 2) + 4 * h32 + (r & 3);
+              if (key >= p.Sk || (CAUSAL && key > qrow)) x = kNegInf;
+            }
+            s[qb][kb][r] = x;
+            mx = fmaxf(mx, x);
+          }
+        }
+        mx = wave_xor32_max(mx);
+        const float m_new = fmaxf(m_i[qb], mx);
+        const float msub = (m_new == kNegInf) ? 0.f : m_new;
+        const float alpha = fast_exp2(m_i[qb] - msub);
+        float rs = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float e = fast_exp2(s[qb][kb][r] - msub);
+            s[qb][kb][r] = e;
+            rs += e;
+          }
+        }
+        l_i[qb] = l_i[qb] * alpha + rs;
+        m_i[qb] = m_new;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) oacc[qb][db] *= alpha;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) pk[qb][st] = pack8<T>(s[qb][st >> 1], 8 * (st & 1));
+      }
+
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const u32x4 a = lds_read_tr_operand(Vs, VSTR, 16 * st, 32 * db, lane);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) oacc[qb][db] = Elem<T>::mfma(a, pk[qb][st], oacc[qb][db]);
+        }
+      }
+    }
+    if (it + 1 < ntiles) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qrow = wq0 + qb * 32 + l32;
+    const float lt = wave_xor32_sum(l_i[qb]);
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    if (qrow < p.Sq) {
+      uint16_t* Op = p.o + b * p.o_sb + h * p.o_sh + qrow * p.o_ss;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d = 32 * db + 8 * g4 + 4 * h32;
+          if (d < p.D) {
+            u32x2 w;
+            w[0] = pack2<T>(oacc[qb][db][4 * g4 + 0] * inv, oacc[qb][db][4 * g4 + 1] * inv);
+            w[1] = pack2<T>(oacc[qb][db][4 * g4 + 2] * inv, oacc[qb][db][4 * g4 + 3] * inv);
+            *reinterpret_cast<u32x2*>(Op + d) = w;
+          }
+        }
+      }
+      if (h32 == 0) {
+        p.lse[((int64_t)b * p.Hq + h) * p.Sq + qrow] =
+            lt > 0.f ? (m_i[qb] + fast_log2(lt)) * kLn2 : kNegInf;
+      }
+    }
+  }
+}
+
+template <typename T, int DT, int QB>
+static int launch_fwd(const FwdParams& prm, bool causal, hipStream_t stream) {
+  FwdParams p = prm;
+  constexpr int BM = 4 * QB * 32;
+  p.nqt = cdiv(p.Sq, BM);
+  const int64_t grid = (int64_t)p.nqt * p.B * p.Hq;
+  if (grid > 0x7fffffff) return set_error(KF_EUNSUPPORTED, "kf_attn_fwd: grid too large");
+  if (causal)
+    hipLaunchKernelGGL((fwd_kernel<T, DT, QB, true>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((fwd_kernel<T, DT, QB, false>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  return check_launch("kf_attn_fwd");
+}
+
+template <typename T>
+static int dispatch_fwd(const FwdParams& p, bool causal, hipStream_t stream) {
+  // Two query blocks per wave halve the LDS traffic per MFMA; use them when the
+  // grid still fills the chip at least twice.
+  const int64_t tiles256 = (int64_t)cdiv(p.Sq, 256) * p.B * p.Hq;
+  const bool qb2 = tiles256 >= 512;
+  switch (head_tile(p.D)) {
+    case 32: return qb2 ? launch_fwd<T, 32, 2>(p, causal, stream) : launch_fwd<T, 32, 1>(p, causal, stream);
+    case 64: return qb2 ? launch_fwd<T, 64, 2>(p, causal, stream) : launch_fwd<T, 64, 1>(p, causal, stream);
+    case 96: return qb2 ? launch_fwd<T, 96, 2>(p, causal, stream) : launch_fwd<T, 96, 1>(p, causal, stream);
+    default: return qb2 ? launch_fwd<T, 128, 2>(p, causal, stream) : launch_fwd<T, 128, 1>(p, causal, stream);
+  }
+}
+
+// Shared argument checks of the attention entry points.
+int check_attn_common(const char* what, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk,
+                      int64_t D, int dtype) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Sq <= 0 || Sk <= 0 || D <= 0)
+    return set_error(KF_EINVAL, "%s: all sizes must be positive", what);
+  if (Hq % Hkv != 0)
+    return set_error(KF_EINVAL, "%s: num_query_heads must be divisible by num_kv_heads", what);
+  if (D % 8 != 0 || D > 128)
+    return set_error(KF_EUNSUPPORTED, "%s: head_dim must be a multiple of 8 in [8, 128], got %lld",
+                     what, (long long)D);
+  if (dtype != KF_F16 && dtype != KF_BF16)
+    return set_error(KF_EINVAL, "%s: dtype must be KF_F16 or KF_BF16", what);
+  if (Sq > 0x3fffffff || Sk > 0x3fffffff || B * Hq > 0x3fffffff)
+    return set_error(KF_EUNSUPPORTED, "%s: sizes exceed the kernels' 32-bit row indexing", what);
+  return KF_OK;
+}
+
+int check_tensor(const char* what, const char* name, const void* ptr, const int64_t* strides) {
+  if (ptr == nullptr) return set_error(KF_EINVAL, "%s: %s is null", what, name);
+  if (strides == nullptr) return set_error(KF_EINVAL, "%s: %s strides are null", what, name);
+  if (!aligned16(ptr)) return set_error(KF_EINVAL, "%s: %s must be 16-byte aligned", what, name);
+  for (int i = 0; i < 3; ++i)
+    if (strides[i] < 0 || strides[i] % 8 != 0)
+      return set_error(KF_EINVAL, "%s: %s strides must be non-negative multiples of 8 elements",
+                       what, name);
+  return KF_OK;
+}
+
+}  // namespace kf
+
+using namespace kf;
+
+extern "C" int kf_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                           int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                           const int64_t* q_strides, const int64_t* k_strides,
+                           const int64_t* v_strides, const int64_t* o_strides, float scale,
+                           int causal, int dtype, void* stream) {
+  const char* what = "kf_attn_fwd";
+  int rc = check_attn_common(what, B, Hq, Hkv, Sq, Sk, D, dtype);
+  if (rc) return rc;
+  if ((rc = check_tensor(what, "q", q, q_strides)) || (rc = check_tensor(what, "k", k, k_strides)) ||
+      (rc = check_tensor(what, "v", v, v_strides)) || (rc = check_tensor(what, "o", o, o_strides)))
+    return rc;
+  if (lse == nullptr) return set_error(KF_EINVAL, "%s: lse is null", what);
+  if (!(scale == scale) || scale - scale != 0.f) return set_error(KF_EINVAL, "%s: scale must be finite", what);
+  FwdParams p{};
+  p.q = (const uint16_t*)q;
+  p.k = (const uint16_t*)k;
+  p.v = (const uint16_t*)v;
+  p.o = (uint16_t*)o;
+  p.lse = lse;
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
+  p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
+  p.v_sb = v_strides[0]; p.v_sh = v_strides[1]; p.v_ss = v_strides[2];
+  p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
+  p.B = (int)B; p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.Sq = (int)Sq; p.Sk = (int)Sk; p.D = (int)D;
+  p.scale_log2 = scale * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  return dtype == KF_F16 ? dispatch_fwd<_Float16>(p, causal != 0, s)
+                         : dispatch_fwd<__bf16>(p, causal != 0, s);
+}

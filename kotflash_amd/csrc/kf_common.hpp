@@ -1,0 +1,140 @@
+// Shared device primitives for the gfx950 (CDNA4) attention kernels.
+//
+// Conventions used by every kernel in this directory:
+//  * Tensors are [batch, heads, sequence, head_dim] with a unit head_dim stride;
+//    the batch/head/sequence strides are passed in elements (int64).
+//  * Head dims are padded at compile time to DT (a multiple of 32). The real
+//    head_dim D is a multiple of 8, so a 16-byte chunk of 8 elements is either
+//    entirely inside [0, D) or entirely padding (zero-filled).
+//  * MFMA is v_mfma_f32_32x32x16_{f16,bf16}. Its operand/result layout, checked
+//    on the device with an in-bounds probe:
+//      A (32 x 16):  lane l holds row  i = l % 32, eight k slots (h = l / 32, t = 0..7)
+//      B (16 x 32):  lane l holds col  j = l % 32, the same eight k slots
+//      C (32 x 32):  lane l, register r holds C[8*(r/4) + 4*(l/32) + r%4][l % 32]
+//    Only the agreement of the A and B k-slots matters, so every kernel assigns
+//    slot (h, t) to whatever contraction index is cheapest to load.
+//  * ds_read_b64_tr_b16 (gfx950), checked the same way: inside each 16-lane
+//    group, lane i element e is element (i % 4) of the 8-byte piece addressed by
+//    lane (i / 4 + 4 e). Giving lane p the address of row (p / 4), columns
+//    4 (p % 4) .. +3 of a row-major 4 x 16 block therefore returns column i of
+//    that block (rows 0..3) to lane i: a transposed read of 16-bit data.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kf {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+#define KF_LDS __attribute__((address_space(3)))
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+// Element traits: storage type, MFMA, float conversion.
+template <typename T> struct Elem;
+
+template <> struct Elem<_Float16> {
+  using v8 = f16x8;
+  __device__ static inline f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint16_t bits(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+  __device__ static inline float to_f32(uint16_t b) {
+    return (float)__builtin_bit_cast(_Float16, b);
+  }
+};
+
+template <> struct Elem<__bf16> {
+  using v8 = bf16x8;
+  __device__ static inline f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint16_t bits(float x) {
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+  __device__ static inline float to_f32(uint16_t b) {
+    return __builtin_bit_cast(float, ((uint32_t)b) << 16);
+  }
+};
+
+template <typename T>
+__device__ inline uint32_t pack2(float lo, float hi) {
+  return (uint32_t)Elem<T>::bits(lo) | ((uint32_t)Elem<T>::bits(hi) << 16);
+}
+
+// Eight consecutive accumulator registers -> one 8-element MFMA operand.
+template <typename T>
+__device__ inline u32x4 pack8(const f32x16& acc, int r0) {
+  u32x4 out;
+  out[0] = pack2<T>(acc[r0 + 0], acc[r0 + 1]);
+  out[1] = pack2<T>(acc[r0 + 2], acc[r0 + 3]);
+  out[2] = pack2<T>(acc[r0 + 4], acc[r0 + 5]);
+  out[3] = pack2<T>(acc[r0 + 6], acc[r0 + 7]);
+  return out;
+}
+
+__device__ inline f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+__device__ inline u32x4 zero_u4() {
+  u32x4 z = {0u, 0u, 0u, 0u};
+  return z;
+}
+
+__device__ inline u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ inline void stg16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+__device__ inline u32x4 lds_read16(const uint16_t* p) {
+  return *(const KF_LDS u32x4*)(p);
+}
+__device__ inline void lds_write16(uint16_t* p, u32x4 v) { *(KF_LDS u32x4*)(p) = v; }
+
+// Transposed LDS read of a 4 x 16 block of 16-bit elements (see header comment).
+__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
+  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((KF_LDS s16x4*)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// MFMA A operand of a transposed row-major LDS tile: lane (i = l % 32, h = l / 32)
+// receives X[row0 + 8u + 4h + e][col0 + i] for slots t = 4u + e.  The row index
+// of slot (h, t) is therefore 8 (t / 4) + 4 h + t % 4 -- the same contraction
+// index an f32x16 accumulator register r = t (+ 8) carries in its row, which is
+// what lets a softmax result feed the next MFMA as a B operand without any data
+// movement.
+__device__ inline u32x4 lds_read_tr_operand(const uint16_t* tile, int stride, int row0, int col0,
+                                            int lane) {
+  const int p = lane & 15;
+  const int h = lane >> 5;
+  const int g = (lane >> 4) & 1;
+  const uint16_t* base = tile + (row0 + 4 * h + (p >> 2)) * stride + col0 + 16 * g + 4 * (p & 3);
+  u32x2 lo = lds_read_tr16(base);
+  u32x2 hi = lds_read_tr16(base + 8 * stride);
+  u32x4 out = {lo[0], lo[1], hi[0], hi[1]};
+  return out;
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+__device__ inline float wave_xor32_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+__device__ inline float wave_xor32_sum(float x) { return x + __shfl_xor(x, 32); }
+
+__host__ __device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace kf

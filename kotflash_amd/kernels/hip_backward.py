@@ -1,0 +1,37 @@
+"""Backward launcher: ``attention_backward`` returning (dq, dk, dv).
+
+Mirrors the reference's ``attention_backward`` (kotflash/kernels/
+triton_backward.py:335-421): gradients are allocated with torch in the input
+dtypes, dK/dV are summed over each GQA group, and the row delta is computed
+from the stored low-precision O. The workspace (fp32 row deltas) comes from
+torch's caching allocator.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _hip
+from ._layout import padded_head_dim, prepare, require_hip_tensors, unpad
+from .hip_forward import _check_shapes
+
+
+def attention_backward(q, k, v, out, lse, grad_out, *, causal: bool, scale: float):
+    require_hip_tensors("HIP attention backward", q, k, v, out, grad_out)
+    _check_shapes(q, k, v)
+    if out.shape != q.shape or grad_out.shape != q.shape:
+        raise ValueError("out and grad_out must have q's shape")
+    if lse.shape != q.shape[:3] or lse.dtype != torch.float32:
+        raise ValueError("lse must be float32 [B, Hq, Sq]")
+    d = q.shape[3]
+    dp = padded_head_dim(d)
+    q_, k_, v_, o_, do_ = (prepare(t, dp) for t in (q, k, v, out, grad_out))
+    lse_ = lse.contiguous()
+    b, hq, sq, _ = q_.shape
+    hkv, sk = k_.shape[1], k_.shape[2]
+    dq = torch.empty_like(q_, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(k_, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v_, memory_format=torch.contiguous_format)
+    nbytes = _hip.bwd_workspace_bytes(b, hq, hkv, sq, sk, dp, causal)
+    ws = torch.empty(max(nbytes, 256), device=q.device, dtype=torch.uint8)
+    _hip.bwd(q_, k_, v_, o_, lse_, do_, dq, dk, dv, causal=causal, scale=scale, workspace=ws)
+    return unpad(dq, d), unpad(dk, d), unpad(dv, d)

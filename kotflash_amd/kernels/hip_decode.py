@@ -1,0 +1,129 @@
+"""Decode launchers for preallocated (possibly padded) K/V caches.
+
+Mirrors the reference's stride-aware decode module (kotflash/kernels/
+triton_decode.py:302-468): ``strided_decode_supported``,
+``attention_forward_strided_decode`` and ``attention_forward_strided_append``,
+plus ``attention_decode_ragged`` for caches whose sequences have different
+lengths (one launch for all of them, keys beyond each sequence's length
+masked).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from .. import _hip
+from .._planning import GFX950_DECODE_MAX_SQ, GFX950_DECODE_MIN_SK, gfx950_head_dim_ok
+from ._layout import padded_head_dim, prepare, require_hip_tensors
+
+
+def strided_decode_supported(q, k, v) -> bool:
+    """Whether the HIP split-KV decode reads these tensors in place: GPU
+    fp16/bf16 on gfx950, a short query (Sq <= 16) against a long key sequence
+    (Sk >= 1024), 8 <= D <= 128 with D a multiple of 8, and layouts with a unit
+    head_dim stride, 8-element multiple strides and 16-byte alignment -- which
+    includes the padded prefix views of ``PreallocatedKVCache`` (reference
+    triton_decode.py:389-409 accepts only D <= 64 and fp16)."""
+    if not all(isinstance(t, torch.Tensor) for t in (q, k, v)):
+        return False
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        return False
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        return False
+    if q.ndim != 4 or k.ndim != 4 or v.shape != k.shape:
+        return False
+    if q.shape[0] != k.shape[0] or q.shape[1] % k.shape[1] or q.shape[3] != k.shape[3]:
+        return False
+    d = q.shape[3]
+    if q.shape[2] > GFX950_DECODE_MAX_SQ or k.shape[2] < GFX950_DECODE_MIN_SK:
+        return False
+    if not gfx950_head_dim_ok(d) or d % 8:
+        return False
+    if not all(_hip.layout_ok(t) for t in (q, k, v)):
+        return False
+    return _hip.is_gfx950(q.device) and _hip.library_available()
+
+
+def _decode(q, k, v, seqlens: Optional[torch.Tensor], scale: float, with_lse: bool):
+    b, hq, sq, d = q.shape
+    hkv, sk = k.shape[1], k.shape[2]
+    out = torch.empty((b, hq, sq, d), device=q.device, dtype=q.dtype)
+    lse = torch.empty((b, hq, sq), device=q.device, dtype=torch.float32) if with_lse else None
+    splits = _hip.decode_num_splits(b, hq, hkv, sq, sk, d)
+    nbytes = _hip.decode_workspace_bytes(b, hq, sq, d, splits)
+    ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8) if nbytes else None
+    _hip.decode(q, k, v, out, lse, seqlens, scale=scale, num_splits=splits, workspace=ws)
+    return out, lse
+
+
+def attention_forward_strided_decode(q, k, v, *, scale: float):
+    """Inference-only split-KV decode reading (padded) K/V views in place;
+    returns O (reference triton_decode.py:412-468)."""
+    if not strided_decode_supported(q, k, v):
+        raise ValueError(
+            "expected fp16/bf16 gfx950 tensors with a short query, a long key "
+            "sequence and an inner-contiguous, 16-byte aligned K/V layout"
+        )
+    return _decode(q, k, v, None, float(scale), with_lse=False)[0]
+
+
+def attention_forward_strided_append(q, k_cache, v_cache, new_k, new_v, *,
+                                     past_length: int, scale: float):
+    """Append one token at ``past_length`` and attend over the first
+    ``past_length + 1`` cache positions; returns O.
+
+    Same contract as the reference (triton_decode.py:302-386). The reference
+    folds the slot write into its split kernel; here the append is its own
+    16-byte-vector copy launch followed by the split-KV decode, which reads
+    the freshly written slot from the cache.
+    """
+    require_hip_tensors("fused append/decode", q, k_cache, v_cache, new_k, new_v)
+    if q.ndim != 4 or q.shape[2] != 1:
+        raise ValueError("q must be [B,Hq,1,D]")
+    if k_cache.ndim != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("K/V cache must have matching [B,Hkv,capacity,D] shapes")
+    if k_cache.stride(3) != 1 or v_cache.stride(3) != 1:
+        raise ValueError("destination K/V cache buffers need a unit head_dim stride")
+    if new_k.ndim != 4 or new_v.shape != new_k.shape or new_k.shape[2] != 1:
+        raise ValueError("new K/V must have matching [B,Hkv,1,D] shapes")
+    b, hq, _, d = q.shape
+    _, hkv, capacity, cache_d = k_cache.shape
+    if cache_d != d or new_k.shape != (b, hkv, 1, d):
+        raise ValueError("query, cache and new K/V shapes are incompatible")
+    if hq % hkv or past_length < 0 or past_length + 1 > capacity:
+        raise ValueError("unsupported head grouping, cache length or capacity")
+    _hip.kv_append(k_cache, v_cache, new_k, new_v, start=past_length)
+    k_view = k_cache[:, :, : past_length + 1]
+    v_view = v_cache[:, :, : past_length + 1]
+    dp = padded_head_dim(d)
+    if dp != d or not all(_hip.layout_ok(t) for t in (q, k_view, v_view)):
+        q, k_view, v_view = (prepare(t, dp) for t in (q, k_view, v_view))
+    out = _decode(q, k_view, v_view, None, float(scale), with_lse=False)[0]
+    return out[..., :d].contiguous() if dp != d else out
+
+
+def attention_decode_ragged(q, k_cache, v_cache, seqlens: torch.Tensor, *, max_seqlen: int,
+                            scale: float, with_lse: bool = False):
+    """Non-causal decode where batch entry b sees cache positions
+    [0, seqlens[b]). ``seqlens`` is a device int32 [B] tensor and
+    ``max_seqlen`` >= max(seqlens) bounds the planned splits. Returns O, or
+    (O, LSE) with ``with_lse``."""
+    require_hip_tensors("ragged decode", q, k_cache, v_cache)
+    if seqlens.dtype != torch.int32 or seqlens.device != q.device or seqlens.shape != (q.shape[0],):
+        raise ValueError("seqlens must be a device int32 tensor of shape [B]")
+    if q.ndim != 4 or k_cache.ndim != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("expected [B,H,S,D] query and cache tensors")
+    if not (0 < max_seqlen <= k_cache.shape[2]):
+        raise ValueError("max_seqlen must be in [1, capacity]")
+    if q.shape[0] != k_cache.shape[0] or q.shape[1] % k_cache.shape[1] or q.shape[3] != k_cache.shape[3]:
+        raise ValueError("query and cache shapes are incompatible")
+    d = q.shape[3]
+    if d % 8 or not gfx950_head_dim_ok(d):
+        raise ValueError("ragged decode needs head_dim a multiple of 8 in [8, 128]")
+    k_view = k_cache[:, :, :max_seqlen]
+    v_view = v_cache[:, :, :max_seqlen]
+    if not all(_hip.layout_ok(t) for t in (q, k_view, v_view)):
+        raise ValueError("ragged decode needs inner-contiguous, 16-byte aligned tensors")
+    out, lse = _decode(q, k_view, v_view, seqlens, float(scale), with_lse=with_lse)
+    return (out, lse) if with_lse else out

@@ -1,0 +1,65 @@
+"""Forward launcher: ``attention_forward`` returning (out, lse).
+
+Mirrors the reference's ``attention_forward`` (kotflash/kernels/
+triton_forward.py:372-456): outputs are allocated with torch (``out`` in the
+input dtype, ``lse`` fp32 [B, Hq, Sq]); a non-causal short-query/long-key
+problem takes the split-KV decode kernel with an LSE merge, everything else the
+MFMA online-softmax forward.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _hip
+from .._planning import gfx950_decode_eligible, gfx950_head_dim_ok
+from ._layout import padded_head_dim, prepare, require_hip_tensors, unpad
+
+
+def hip_available() -> bool:
+    """True when the HIP library loads and the current device is gfx950."""
+    if not torch.cuda.is_available() or not _hip.library_available():
+        return False
+    return _hip.is_gfx950(torch.device("cuda", torch.cuda.current_device()))
+
+
+def triton_available() -> bool:
+    """Kept for import compatibility with the reference API: this build has no
+    Triton kernels."""
+    return False
+
+
+def triton_turing_supported() -> bool:
+    """Kept for import compatibility: always False (no Triton, no SM75)."""
+    return False
+
+
+def _check_shapes(q, k, v) -> None:
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("Expected q/k/v in [batch, heads, sequence, head_dim] layout")
+    if k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[3] != k.shape[3]:
+        raise ValueError("incompatible q/k/v shapes")
+    if q.shape[1] % k.shape[1] != 0:
+        raise ValueError("num_query_heads must be divisible by num_kv_heads (GQA/MQA)")
+    if not gfx950_head_dim_ok(q.shape[3]):
+        raise ValueError("HIP backend supports 8 <= head_dim <= 128")
+
+
+def attention_forward(q, k, v, *, causal: bool, scale: float):
+    """Run the HIP forward; returns ``(out, lse)``."""
+    require_hip_tensors("HIP attention forward", q, k, v)
+    _check_shapes(q, k, v)
+    d = q.shape[3]
+    dp = padded_head_dim(d)
+    q_, k_, v_ = (prepare(t, dp) for t in (q, k, v))
+    b, hq, sq, _ = q_.shape
+    hkv, sk = k_.shape[1], k_.shape[2]
+    out = torch.empty((b, hq, sq, dp), device=q.device, dtype=q.dtype)
+    lse = torch.empty((b, hq, sq), device=q.device, dtype=torch.float32)
+    if gfx950_decode_eligible(sq, sk, dp, causal=causal):
+        splits = _hip.decode_num_splits(b, hq, hkv, sq, sk, dp)
+        nbytes = _hip.decode_workspace_bytes(b, hq, sq, dp, splits)
+        ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8) if nbytes else None
+        _hip.decode(q_, k_, v_, out, lse, None, scale=scale, num_splits=splits, workspace=ws)
+    else:
+        _hip.fwd(q_, k_, v_, out, lse, causal=causal, scale=scale)
+    return unpad(out, d), lse
