@@ -1,0 +1,112 @@
+"""The C-ABI library: it loads, exports every entry point the header declares,
+the ctypes signatures cover exactly those, and argument validation (which runs
+before any GPU work) reports errors through kf_last_error. No kernel is
+launched here."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from kotflash_amd import _hip
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "kotflash_amd.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\*?\s+\*?(kf_[a-z_0-9]+)\(", text, re.M)))
+
+
+def test_header_declares_the_expected_entry_points():
+    assert header_functions() == sorted(_hip.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _hip.lib()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_hip.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r" T (kf_[a-z_0-9]+)$", out, re.M))
+    assert set(header_functions()) <= exported
+
+
+def test_abi_version():
+    assert _hip.lib().kf_abi_version() == _hip.ABI_VERSION
+
+
+def test_library_has_gfx950_code_object_only():
+    out = subprocess.run(["strings", str(_hip.LIB_PATH)], capture_output=True, text=True).stdout
+    assert "gfx950" in out
+    assert "sm_" not in re.findall(r"amdgcn-amd-amdhsa--(\w+)", out)
+
+
+def _arr(*vals):
+    return ctypes.cast((ctypes.c_int64 * len(vals))(*vals), _hip._I64P)
+
+
+@pytest.mark.parametrize("kwargs,match", [
+    (dict(B=0), "positive"),
+    (dict(Hq=3, Hkv=2), "divisible"),
+    (dict(D=72 + 4), "multiple of 8"),
+    (dict(D=136), "multiple of 8"),
+    (dict(dtype=7), "dtype"),
+    (dict(q=None), "q is null"),
+    (dict(q=0x1008), "aligned"),
+    (dict(scale=float("inf")), "finite"),
+])
+def test_fwd_argument_validation(kwargs, match):
+    a = dict(q=0x1000, k=0x2000, v=0x3000, o=0x4000, lse=0x5000, B=1, Hq=2, Hkv=1, Sq=4, Sk=4,
+             D=64, dtype=0, scale=0.125)
+    a.update(kwargs)
+    s = _arr(512, 256, 64)
+    rc = _hip.lib().kf_attn_fwd(a["q"], a["k"], a["v"], a["o"], a["lse"], a["B"], a["Hq"], a["Hkv"],
+                                a["Sq"], a["Sk"], a["D"], s, s, s, s, a["scale"], 0, a["dtype"], None)
+    assert rc != 0
+    assert match in _hip.lib().kf_last_error().decode()
+
+
+def test_bad_strides_rejected():
+    s_ok = _arr(512, 256, 64)
+    s_bad = _arr(512, 256, 63)
+    rc = _hip.lib().kf_attn_fwd(0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 1, 2, 1, 4, 4, 64,
+                                s_bad, s_ok, s_ok, s_ok, 0.1, 0, 0, None)
+    assert rc == 1 and "strides" in _hip.lib().kf_last_error().decode()
+
+
+def test_bwd_requires_workspace():
+    s = _arr(512, 256, 64)
+    rc = _hip.lib().kf_attn_bwd(*([0x1000] * 9), 1, 2, 1, 4, 4, 64, *([s] * 8), 0.1, 1, 0, None, 0, None)
+    assert rc == 1 and "workspace" in _hip.lib().kf_last_error().decode()
+    assert _hip.lib().kf_attn_bwd_workspace_bytes(2, 16, 4, 4096, 4096, 128, 1) >= 2 * 16 * 4096 * 4
+
+
+def test_decode_planner_and_workspace():
+    lib = _hip.lib()
+    for sk in (2048, 4096, 8192, 16384, 1537, 8193, 100000):
+        ns = lib.kf_decode_num_splits(2, 8, 2, 1, sk, 64)
+        chunk = ((-(-sk // ns)) + 127) // 128 * 128
+        assert ns >= 1 and -(-sk // chunk) == ns
+    assert lib.kf_decode_num_splits(2, 8, 2, 1, 16384, 64) == 128
+    assert lib.kf_decode_workspace_bytes(2, 8, 1, 64, 1) == 0
+    assert lib.kf_decode_workspace_bytes(2, 8, 1, 64, 128) >= 128 * 16 * 65 * 4
+    s = _arr(512, 64, 64)
+    rc = lib.kf_attn_decode(0x1000, 0x2000, 0x3000, 0x4000, None, None, 2, 8, 2, 1, 16384, 64,
+                            s, s, s, s, 0.125, 127, 0, None, 0, None)
+    assert rc == 1 and "partition" in lib.kf_last_error().decode()
+    rc = lib.kf_attn_decode(0x1000, 0x2000, 0x3000, 0x4000, None, None, 2, 8, 2, 1, 16384, 64,
+                            s, s, s, s, 0.125, 128, 0, None, 0, None)
+    assert rc == 1 and "workspace" in lib.kf_last_error().decode()
+
+
+def test_append_argument_validation():
+    lib = _hip.lib()
+    s3 = _arr(64 * 8, 64 * 8, 8)
+    s4 = _arr(2 * 8, 8, 8, 1)
+    rc = lib.kf_kv_append(0x1000, 0x2000, 0x3000, 0x4000, None, 62, 1, 1, 3, 8, 64, s3, s3, s4, s4, 0, None)
+    assert rc == 1 and "capacity" in lib.kf_last_error().decode()
+    rc = lib.kf_kv_append(None, 0x2000, 0x3000, 0x4000, None, 0, 1, 1, 3, 8, 64, s3, s3, s4, s4, 0, None)
+    assert rc == 1 and "null" in lib.kf_last_error().decode()

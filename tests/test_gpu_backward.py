@@ -1,0 +1,173 @@
+"""Backward parity on the GPU: HIP dQ/dK/dV (through the C ABI) vs the
+golden fixtures, the oracle and fp32 autograd, including GQA group sums,
+head-dim tails and the BASELINE configurations."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from kotflash_amd import attention
+from kotflash_amd.kernels.hip_backward import attention_backward
+from kotflash_amd.kernels.hip_forward import attention_forward
+from oracle import attention_oracle as orc
+from tests.conftest import GOLDEN_ATTN_CASES
+from tests.gpu_helpers import BWD_TOL, FWD_TOL, assert_close, reference_fp32, seeded
+
+pytestmark = pytest.mark.gpu
+F16, BF16 = torch.float16, torch.bfloat16
+
+
+def _check_grads(q, k, v, do, causal, dtype, what):
+    out, lse = attention_forward(q, k, v, causal=causal, scale=1 / math.sqrt(q.shape[-1]))
+    dq, dk, dv = attention_backward(q, k, v, out, lse, do, causal=causal,
+                                    scale=1 / math.sqrt(q.shape[-1]))
+    eo, el, (eq, ek, ev) = reference_fp32(q, k, v, causal=causal, with_grad_out=do)
+    assert dq.dtype == q.dtype and dk.shape == k.shape and dv.shape == v.shape
+    assert_close(out, eo, **FWD_TOL[dtype], what=f"{what} O")
+    assert_close(dq, eq, **BWD_TOL[dtype], what=f"{what} dQ")
+    assert_close(dk, ek, **BWD_TOL[dtype], what=f"{what} dK")
+    assert_close(dv, ev, **BWD_TOL[dtype], what=f"{what} dV")
+
+
+@pytest.mark.parametrize("name", GOLDEN_ATTN_CASES)
+def test_backward_matches_golden(golden, name):
+    b, hq, hkv, sq, sk, d, causal = (int(x) for x in golden[f"{name}/meta"])
+    q, k, v, do = (torch.from_numpy(golden[f"{name}/{x}"]).cuda() for x in ("q", "k", "v", "do"))
+    out, lse = attention_forward(q, k, v, causal=bool(causal), scale=1 / math.sqrt(d))
+    dq, dk, dv = attention_backward(q, k, v, out, lse, do, causal=bool(causal), scale=1 / math.sqrt(d))
+    for got, key in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+        assert_close(got, torch.from_numpy(golden[f"{name}/{key}"]), **BWD_TOL[F16],
+                     what=f"{name} {key}")
+
+
+def test_backward_matches_oracle_with_stored_o():
+    """The oracle restates the kernels' numerics: delta from the stored fp16 O
+    and the kernel's own LSE, P and dS rounded to fp16 before their products."""
+    q = seeded((1, 4, 150, 64), 71, dtype=F16)
+    k = seeded((1, 2, 170, 64), 72, dtype=F16)
+    v = seeded((1, 2, 170, 64), 73, dtype=F16)
+    do = seeded((1, 4, 150, 64), 74, dtype=F16)
+    out, lse = attention_forward(q, k, v, causal=True, scale=0.125)
+    dq, dk, dv = attention_backward(q, k, v, out, lse, do, causal=True, scale=0.125)
+    n = lambda t: t.detach().cpu().float().numpy().astype(np.float64)
+    eq, ek, ev = orc.backward_blockwise(n(q), n(k), n(v), n(out), n(lse), n(do), causal=True,
+                                        scale=0.125, p_dtype=np.float16)
+    for got, exp, key in ((dq, eq, "dq"), (dk, ek, "dk"), (dv, ev, "dv")):
+        assert_close(got, torch.from_numpy(exp), atol=4e-3, rtol=4e-3, what=key)
+
+
+@pytest.mark.parametrize("hq,hkv,sq,sk,d,causal", [
+    # The reference's backward cases (tests/test_triton.py:160-174).
+    (4, 4, 64, 80, 32, False),
+    (8, 2, 64, 80, 64, True),
+    (8, 1, 80, 64, 32, True),
+    (8, 2, 48, 64, 72, False),
+    (4, 4, 48, 64, 96, True),
+    (8, 1, 64, 48, 128, False),
+    (8, 2, 1024, 1024, 64, True),
+    (4, 1, 1024, 768, 32, False),
+    (4, 2, 2048, 2048, 32, True),
+    (8, 2, 1, 1024, 64, False),
+])
+@pytest.mark.parametrize("dtype", [F16, BF16])
+def test_backward_reference_cases(hq, hkv, sq, sk, d, causal, dtype):
+    q = seeded((1, hq, sq, d), 12, dtype=dtype)
+    k = seeded((1, hkv, sk, d), 13, dtype=dtype)
+    v = seeded((1, hkv, sk, d), 14, dtype=dtype)
+    do = seeded((1, hq, sq, d), 15, dtype=dtype)
+    _check_grads(q, k, v, do, causal, dtype, f"{(hq, hkv, sq, sk, d, causal)}")
+
+
+@pytest.mark.parametrize("shape", [
+    (1, 2, 1, 500, 130, 64, True),   # Sq > Sk causal: keys seen by many rows
+    (1, 2, 2, 70, 900, 128, True),   # keys beyond Sq never seen: zero dK/dV
+    (2, 3, 1, 129, 131, 40, False),  # head_dim 40, ragged tiles
+    (1, 2, 1, 33, 47, 20, True),     # padded head_dim
+])
+def test_backward_edge_shapes(shape):
+    b, hq, hkv, sq, sk, d, causal = shape
+    q = seeded((b, hq, sq, d), 81, dtype=F16)
+    k = seeded((b, hkv, sk, d), 82, dtype=F16)
+    v = seeded((b, hkv, sk, d), 83, dtype=F16)
+    do = seeded((b, hq, sq, d), 84, dtype=F16)
+    _check_grads(q, k, v, do, causal, F16, f"{shape}")
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16])
+def test_config3_forward_backward(dtype):
+    """B=2, Hq=16, Hkv=4, S=4096, D=128, causal,
+    q/k/v ~ 0.5 N(0,1), dO ~ N(0,1); dK/dV summed over the GQA group."""
+    q = seeded((2, 16, 4096, 128), 301, dtype=dtype, scale=0.5)
+    k = seeded((2, 4, 4096, 128), 302, dtype=dtype, scale=0.5)
+    v = seeded((2, 4, 4096, 128), 303, dtype=dtype, scale=0.5)
+    do = seeded((2, 16, 4096, 128), 304, dtype=dtype)
+    _check_grads(q, k, v, do, True, dtype, "cfg3")
+
+
+@pytest.mark.parametrize("head_dim", [72, 96])
+def test_config4_forward_backward(head_dim):
+    """B=4, H=12, S=2048, D in {72, 96}, non-causal MHA."""
+    q = seeded((4, 12, 2048, head_dim), 401, dtype=F16)
+    k = seeded((4, 12, 2048, head_dim), 402, dtype=F16)
+    v = seeded((4, 12, 2048, head_dim), 403, dtype=F16)
+    do = seeded((4, 12, 2048, head_dim), 404, dtype=F16)
+    _check_grads(q, k, v, do, False, F16, f"cfg4 D={head_dim}")
+
+
+def test_backward_is_deterministic():
+    q = seeded((1, 8, 700, 64), 91, dtype=F16)
+    k = seeded((1, 2, 700, 64), 92, dtype=F16)
+    v = seeded((1, 2, 700, 64), 93, dtype=F16)
+    do = seeded((1, 8, 700, 64), 94, dtype=F16)
+    out, lse = attention_forward(q, k, v, causal=True, scale=0.125)
+    a = attention_backward(q, k, v, out, lse, do, causal=True, scale=0.125)
+    b = attention_backward(q, k, v, out, lse, do, causal=True, scale=0.125)
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16])
+def test_autograd_through_public_api(dtype):
+    q = seeded((1, 4, 96, 64), 95, dtype=dtype).requires_grad_(True)
+    k = seeded((1, 2, 96, 64), 96, dtype=dtype).requires_grad_(True)
+    v = seeded((1, 2, 96, 64), 97, dtype=dtype).requires_grad_(True)
+    do = seeded((1, 4, 96, 64), 98, dtype=dtype)
+    out = attention(q, k, v, causal=True, backend="hip")
+    grads = torch.autograd.grad(out, (q, k, v), do)
+    _, _, exp = reference_fp32(q, k, v, causal=True, with_grad_out=do)
+    for g, e, n in zip(grads, exp, "qkv"):
+        assert_close(g, e, **BWD_TOL[dtype], what=f"d{n}")
+    # Short query with grad goes through the split-KV forward + backward.
+    qs = seeded((1, 4, 3, 64), 99, dtype=dtype).requires_grad_(True)
+    ks = seeded((1, 2, 2048, 64), 100, dtype=dtype).requires_grad_(True)
+    vs = seeded((1, 2, 2048, 64), 101, dtype=dtype).requires_grad_(True)
+    dos = seeded((1, 4, 3, 64), 102, dtype=dtype)
+    outs = attention(qs, ks, vs, causal=False, backend="hip")
+    grads = torch.autograd.grad(outs, (qs, ks, vs), dos)
+    _, _, exp = reference_fp32(qs, ks, vs, causal=False, with_grad_out=dos)
+    for g, e, n in zip(grads, exp, "qkv"):
+        assert_close(g, e, **BWD_TOL[dtype], what=f"split d{n}")
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 2, 64, 80, 64, True), (1, 8, 1, 80, 64, 32, True),
+                                   (1, 4, 2, 2048, 2048, 32, True)])
+def test_bf16_gradients_no_worse_than_torch(shape):
+    """bf16 error of the HIP backward vs fp32 stays within PyTorch's own bf16
+    SDPA backward error on the same inputs (x1.25 + 2e-3)."""
+    b, hq, hkv, sq, sk, d, causal = shape
+    q = seeded((b, hq, sq, d), 12, dtype=BF16)
+    k = seeded((b, hkv, sk, d), 13, dtype=BF16)
+    v = seeded((b, hkv, sk, d), 14, dtype=BF16)
+    do = seeded((b, hq, sq, d), 15, dtype=BF16)
+    out, lse = attention_forward(q, k, v, causal=causal, scale=1 / math.sqrt(d))
+    ours = attention_backward(q, k, v, out, lse, do, causal=causal, scale=1 / math.sqrt(d))
+    _, _, exact = reference_fp32(q, k, v, causal=causal, with_grad_out=do)
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    g = hq // hkv
+    to = torch.nn.functional.scaled_dot_product_attention(
+        qq, kk.repeat_interleave(g, 1), vv.repeat_interleave(g, 1), is_causal=causal)
+    theirs = torch.autograd.grad(to, (qq, kk, vv), do)
+    for a, t, e, n in zip(ours, theirs, exact, "qkv"):
+        ea = float((a.float() - e).abs().max())
+        et = float((t.float() - e).abs().max())
+        assert ea <= 1.25 * et + 2e-3, f"d{n}: ours {ea:.4f} vs torch {et:.4f}"
