@@ -1,0 +1,297 @@
+#!/usr/bin/env python3
+"""Headline benchmark of the kotflash_amd attention hot path on one MI355X.
+
+One JSON line on stdout (everything else goes to stderr):
+
+* ``value``: causal GQA fwd+bwd TFLOP/s at BASELINE config 3 (B=2, Hq=16,
+  Hkv=4, S=4096, D=128, fp16, q/k/v ~ 0.5 N(0,1), dO ~ N(0,1)). A step is one
+  forward plus one backward (4 launches: forward, row delta, dQ, dK/dV) on
+  inputs already resident in HBM; exactly ``--steps`` steps are timed between
+  two ``torch.cuda.synchronize()``. Work per step is the algorithmic
+  4.8115e11 FLOP (forward 4 D B Hq S(S+1)/2, backward 2.5x that).
+* ``roofline``: the dominant kernel (the dK/dV kernel), its algorithmic
+  FLOP per launch (the 4 of the 5 backward GEMMs it computes:
+  S = Q K^T, dP = dO V^T, dV, dK = 2x the forward FLOP = 2.7494e11) over its
+  average launch time, from HIP events recorded around it on its launch
+  stream during the timed steps; peak = MI355X dense fp16 MFMA 2.5 PFLOP/s.
+* ``kernels``: the same live figures for every launch of the step.
+* ``decode``: BASELINE config 2 at Sk=16384 (B=2, Hq=8, Hkv=2, Sq=1, D=64,
+  fp16): microseconds per call (split-KV kernel + LSE merge) from HIP-graph
+  replays of back-to-back calls over 32 rotating K/V sets (537 MB, larger than
+  the 256 MB Infinity Cache), and HBM GB/s of the 16,781,376 algorithmic bytes.
+* ``cpu_baseline``: the reference's SDPA path (native-GQA
+  scaled_dot_product_attention, fp32, autograd backward) on the host CPU at the
+  full config 3 shape, median of 3 timed steps after one warm-up.
+
+``--gpus N`` with N > 1 exits with status 2: this build runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+METRIC = "fwd+bwd TFLOP/s at S=4096,D=128; split-KV decode µs/token + HBM GB/s"
+CFG3 = dict(B=2, Hq=16, Hkv=4, S=4096, D=128)
+CFG2 = dict(B=2, Hq=8, Hkv=2, Sq=1, Sk=16384, D=64)
+PEAK_MFMA_F16 = 2.5e15
+PEAK_HBM = 8.0e12
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def fwd_flops(b, hq, s, d):
+    return 4.0 * d * b * hq * s * (s + 1) / 2.0
+
+
+def seeded(torch, shape, seed, dtype, scale=1.0, device="cuda"):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype).to(device)
+
+
+def bench_train(torch, _hip, dtype, steps, warmup):
+    c = CFG3
+    b, hq, hkv, s, d = c["B"], c["Hq"], c["Hkv"], c["S"], c["D"]
+    scale = 1.0 / math.sqrt(d)
+    q = seeded(torch, (b, hq, s, d), 301, dtype, 0.5)
+    k = seeded(torch, (b, hkv, s, d), 302, dtype, 0.5)
+    v = seeded(torch, (b, hkv, s, d), 303, dtype, 0.5)
+    do = seeded(torch, (b, hq, s, d), 304, dtype)
+    out = torch.empty_like(q)
+    lse = torch.empty((b, hq, s), device=q.device, dtype=torch.float32)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = torch.empty(_hip.bwd_workspace_bytes(b, hq, hkv, s, s, d, True), device=q.device,
+                     dtype=torch.uint8)
+    names = ("attn_fwd", "bwd_delta", "bwd_dq", "bwd_dkdv")
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record()
+        _hip.fwd(q, k, v, out, lse, causal=True, scale=scale)
+        if ev is not None:
+            ev[1].record()
+        for i, st in enumerate((_hip.KF_BWD_DELTA, _hip.KF_BWD_DQ, _hip.KF_BWD_DKDV)):
+            _hip.bwd(q, k, v, out, lse, do, dq, dk, dv, causal=True, scale=scale,
+                     workspace=ws, stages=st)
+            if ev is not None:
+                ev[2 + i].record()
+
+    for _ in range(warmup):
+        step()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(steps):
+        step(evs[i])
+    stop.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    ms = start.elapsed_time(stop) / steps
+    per = {n: statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs) for j, n in enumerate(names)}
+    f = fwd_flops(b, hq, s, d)
+    work = {"attn_fwd": f, "bwd_delta": 0.0, "bwd_dq": 0.5 * f, "bwd_dkdv": 2.0 * f}
+    return ms, wall_ms, per, work, 3.5 * f
+
+
+def bench_api(torch, kf, dtype, steps, warmup):
+    """Same step through the public API: attention(backend="hip") + autograd."""
+    c = CFG3
+    q = seeded(torch, (c["B"], c["Hq"], c["S"], c["D"]), 301, dtype, 0.5).requires_grad_(True)
+    k = seeded(torch, (c["B"], c["Hkv"], c["S"], c["D"]), 302, dtype, 0.5).requires_grad_(True)
+    v = seeded(torch, (c["B"], c["Hkv"], c["S"], c["D"]), 303, dtype, 0.5).requires_grad_(True)
+    do = seeded(torch, (c["B"], c["Hq"], c["S"], c["D"]), 304, dtype)
+
+    def step():
+        out = kf.attention(q, k, v, causal=True, backend="hip")
+        torch.autograd.grad(out, (q, k, v), do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def bench_decode(torch, _hip, dtype, sk, replays=20):
+    c = dict(CFG2, Sk=sk)
+    b, hq, hkv, sq, d = c["B"], c["Hq"], c["Hkv"], c["Sq"], c["D"]
+    nsets = 32
+    ks = [seeded(torch, (b, hkv, sk, d), 1000 + i, dtype) for i in range(nsets)]
+    vs = [seeded(torch, (b, hkv, sk, d), 2000 + i, dtype) for i in range(nsets)]
+    q = seeded(torch, (b, hq, sq, d), 3000, dtype)
+    out = torch.empty_like(q)
+    lse = torch.empty((b, hq, sq), device=q.device, dtype=torch.float32)
+    splits = _hip.decode_num_splits(b, hq, hkv, sq, sk, d)
+    ws = torch.empty(max(256, _hip.decode_workspace_bytes(b, hq, hkv, sq, d, splits)), device=q.device,
+                     dtype=torch.uint8)
+
+    def calls():
+        for i in range(nsets):
+            _hip.decode(q, ks[i], vs[i], out, lse, None, scale=1.0 / math.sqrt(d),
+                        num_splits=splits, workspace=ws)
+
+    calls()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        calls()  # warm on the capture stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            calls()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(stop) * 1e3 / (replays * nsets)
+    nbytes = 2 * b * hkv * sk * d * 2 + b * hq * sq * d * 2 * 2 + b * hq * sq * 4
+    return dict(workload=f"B={b} Hq={hq} Hkv={hkv} Sq={sq} Sk={sk} D={d} fp16 non-causal",
+                num_splits=splits, us_per_call=us, us_per_token=us / sq,
+                batch_tokens_per_s=b * sq / (us * 1e-6), algorithmic_bytes=nbytes,
+                hbm_gbps=nbytes / (us * 1e-6) / 1e9, hbm_frac=nbytes / (us * 1e-6) / PEAK_HBM,
+                timing="HIP graph replays of 32 back-to-back calls over 32 K/V sets (537 MB)")
+
+
+def cpu_baseline(dtype_name):
+    """The reference's SDPA path on host cores (fp32, native GQA, autograd
+    backward), timed by the oracle's restatement of it at the config 3 shape."""
+    import torch
+    from oracle.attention_oracle import sdpa_cpu
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    c = CFG3
+    g = torch.Generator().manual_seed(301)
+    q = (torch.randn(c["B"], c["Hq"], c["S"], c["D"], generator=g) * 0.5).to(
+        getattr(torch, dtype_name)).float().requires_grad_(True)
+    k = (torch.randn(c["B"], c["Hkv"], c["S"], c["D"], generator=g) * 0.5).to(
+        getattr(torch, dtype_name)).float().requires_grad_(True)
+    v = (torch.randn(c["B"], c["Hkv"], c["S"], c["D"], generator=g) * 0.5).to(
+        getattr(torch, dtype_name)).float().requires_grad_(True)
+    do = torch.randn(c["B"], c["Hq"], c["S"], c["D"], generator=g)
+
+    def step():
+        out = sdpa_cpu(q, k, v, causal=True)
+        torch.autograd.grad(out, (q, k, v), do)
+
+    step()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    work = 3.5 * fwd_flops(c["B"], c["Hq"], c["S"], c["D"])
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": work / t / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": (f"full config 3 shape (B=2 Hq=16 Hkv=4 S=4096 D=128 causal), fp32 "
+                       f"torch SDPA fwd + autograd bwd as the reference's _sdpa path "
+                       f"(oracle.sdpa_cpu), median of 3 steps = {t:.3f} s on {cores} "
+                       f"threads of {model or 'the host CPU'}")}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n", 1)[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--dtype", choices=("float16", "bfloat16"), default="float16")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(see DESIGN.md for how the path would shard)", file=sys.stderr)
+        return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import torch
+
+    import kotflash_amd as kf
+    from kotflash_amd import _hip
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    dtype = getattr(torch, args.dtype)
+    _hip.lib()
+    log(f"device: {torch.cuda.get_device_properties(0).gcnArchName}")
+
+    ms, wall_ms, per, work, step_flops = bench_train(torch, _hip, dtype, args.steps, args.warmup)
+    log(f"train step: {ms:.4f} ms (GPU events), {wall_ms:.4f} ms (wall); per kernel {per}")
+    api_ms = bench_api(torch, kf, dtype, max(5, args.steps // 5), 2)
+    log(f"public API step: {api_ms:.4f} ms")
+    kernels = {}
+    for n, t in per.items():
+        kernels[n] = {"ms": t, "tflops": work[n] / (t * 1e-3) / 1e12 if work[n] else None,
+                      "frac": work[n] / (t * 1e-3) / PEAK_MFMA_F16 if work[n] else None}
+    dom = "bwd_dkdv"
+    dom_t = per[dom] * 1e-3
+    roofline = {"kernel": "dkdv_kernel (dK/dV, key-stationary backward)", "bound": "mfma",
+                "achieved": work[dom] / dom_t / 1e12, "peak": PEAK_MFMA_F16 / 1e12,
+                "unit": "TFLOP/s", "frac": work[dom] / dom_t / PEAK_MFMA_F16, "traffic": None,
+                "work_per_launch": work[dom],
+                "avg_launch_ms": per[dom]}
+    decode = None if args.no_decode else bench_decode(torch, _hip, torch.float16, CFG2["Sk"])
+    if decode:
+        log(f"decode: {decode}")
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.dtype)
+    value = step_flops / (ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if args.dtype == "float16" else "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5 q/k/v, N(0,1) dO)",
+        "config": {"workload": "BASELINE config 3: causal GQA fwd+bwd B=2 Hq=16 Hkv=4 "
+                               "Sq=Sk=4096 D=128", "global_batch": CFG3["B"], "seq_len": CFG3["S"],
+                   "parallelism": "single GPU"},
+        "frac_of_peak": value * 1e12 / PEAK_MFMA_F16,
+        "wall_ms_per_step": wall_ms,
+        "api_ms_per_step": api_ms,
+        "kernels": kernels,
+        "roofline": roofline,
+        "decode": decode,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -82,21 +82,45 @@ int kf_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
                 size_t workspace_bytes, void* stream);
 
 /*
+ * The three launches of kf_attn_bwd, selectable by a mask of KF_BWD_* bits and
+ * run in the order delta, dq, dkdv (the delta stage writes the fp32 row deltas
+ * into the workspace; dq and dkdv read them). kf_attn_bwd is this call with all
+ * three bits. Same launch split as the reference backward, whose dQ and dK/dV
+ * kernels are separate launches (triton_backward.py:374-419); used to time
+ * each kernel on its own.
+ */
+enum kf_bwd_stage { KF_BWD_DELTA = 1, KF_BWD_DQ = 2, KF_BWD_DKDV = 4 };
+int kf_attn_bwd_stages(int stages, const void* q, const void* k, const void* v, const void* o,
+                       const float* lse, const void* dout, void* dq, void* dk, void* dv,
+                       int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                       const int64_t* q_strides, const int64_t* k_strides,
+                       const int64_t* v_strides, const int64_t* o_strides,
+                       const int64_t* do_strides, const int64_t* dq_strides,
+                       const int64_t* dk_strides, const int64_t* dv_strides, float scale,
+                       int causal, int dtype, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/*
  * Number of KV splits the gfx950 decode planner picks for a short-query,
- * long-cache problem (keys per split are a multiple of 64).
+ * long-cache problem: about one workgroup per CU, each split a whole number of
+ * key stages (256 keys for D <= 64, 128 above). kf_attn_decode accepts any
+ * count whose rounded chunk partitions Sk into exactly that many splits.
  */
 int kf_decode_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D);
 
-/* Workspace for kf_attn_decode in bytes (fp32 partial O and LSE per split). */
-size_t kf_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Sq, int64_t D, int num_splits);
+/* Workspace for kf_attn_decode in bytes (fp32 partial O and LSE per split);
+ * 0 when num_splits == 1. */
+size_t kf_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t D,
+                                 int num_splits);
 
 /*
  * Split-KV decode, non-causal: every query row sees keys [0, L_b) of its
  * batch entry, L_b = seqlens_k[b] (device int32, nullable: L_b = Sk for all b).
  * K/V may be strided prefix views of a larger cache (sequence stride >= D).
  * Each workgroup reads one KV chunk of one (batch, kv_head) once for all
- * Hq/Hkv * Sq query rows; a second kernel merges the per-split (O, LSE)
- * partials with LSE weights. lse is nullable.
+ * Hq/Hkv * Sq query rows and writes an fp32 (O, LSE) partial into the
+ * workspace; a second launch merges the partials with LSE weights (one launch
+ * when num_splits == 1). lse is nullable.
  * Replaces attention_forward_strided_decode + _strided_decode_split /
  * _strided_decode_reduce (reference kotflash/kernels/triton_decode.py:412-468,
  * :16-104, :241-297) and the split-KV branch of attention_forward

@@ -21,6 +21,8 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "libkotflash_amd.so"
 ABI_VERSION = 1
 KF_F16, KF_BF16 = 0, 1
+KF_BWD_DELTA, KF_BWD_DQ, KF_BWD_DKDV = 1, 2, 4
+KF_BWD_ALL = KF_BWD_DELTA | KF_BWD_DQ | KF_BWD_DKDV
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -38,8 +40,11 @@ _SIGNATURES = {
     "kf_attn_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                          _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P,
                          _F, _I, _I, _P, _SZ, _P]),
+    "kf_attn_bwd_stages": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                _I64, _I64, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P,
+                                _I64P, _F, _I, _I, _P, _SZ, _P]),
     "kf_decode_num_splits": (_I, [_I64, _I64, _I64, _I64, _I64, _I64]),
-    "kf_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I]),
+    "kf_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I]),
     "kf_attn_decode": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                             _I64P, _I64P, _I64P, _I64P, _F, _I, _I, _P, _SZ, _P]),
     "kf_kv_append": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
@@ -139,13 +144,13 @@ def bwd_workspace_bytes(b, hq, hkv, sq, sk, d, causal) -> int:
 
 
 def bwd(q, k, v, out, lse, dout, dq, dk, dv, *, causal: bool, scale: float,
-        workspace: torch.Tensor) -> None:
+        workspace: torch.Tensor, stages: int = KF_BWD_ALL) -> None:
     b, hq, sq, d = q.shape
     _, hkv, sk, _ = k.shape
     keep = [_strides(t) for t in (q, k, v, out, dout, dq, dk, dv)]
     with torch.cuda.device(q.device):
-        rc = lib().kf_attn_bwd(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+        rc = lib().kf_attn_bwd_stages(
+            int(stages), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
             dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
             b, hq, hkv, sq, sk, d, *(s[0] for s in keep),
             float(scale), int(bool(causal)), dtype_code(q.dtype),
@@ -159,8 +164,8 @@ def decode_num_splits(b, hq, hkv, sq, sk, d) -> int:
     return int(lib().kf_decode_num_splits(b, hq, hkv, sq, sk, d))
 
 
-def decode_workspace_bytes(b, hq, sq, d, num_splits) -> int:
-    return int(lib().kf_decode_workspace_bytes(b, hq, sq, d, num_splits))
+def decode_workspace_bytes(b, hq, hkv, sq, d, num_splits) -> int:
+    return int(lib().kf_decode_workspace_bytes(b, hq, hkv, sq, d, num_splits))
 
 
 def decode(q, k, v, out, lse: Optional[torch.Tensor], seqlens: Optional[torch.Tensor], *,

@@ -450,36 +450,44 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
 }
 
 template <typename T, int DT>
-static int launch_bwd(BwdParams p, bool causal, hipStream_t stream) {
-  const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
-  hipLaunchKernelGGL((delta_kernel<T>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, stream, p);
-  int rc = check_launch("kf_attn_bwd(delta)");
-  if (rc) return rc;
-  p.nqt = cdiv(p.Sq, 128);
-  const int64_t gq = (int64_t)p.nqt * p.B * p.Hq;
-  if (causal)
-    hipLaunchKernelGGL((dq_kernel<T, DT, true>), dim3((unsigned)gq), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL((dq_kernel<T, DT, false>), dim3((unsigned)gq), dim3(256), 0, stream, p);
-  rc = check_launch("kf_attn_bwd(dq)");
-  if (rc) return rc;
-  p.nqt = cdiv(p.Sq, 64);
-  p.nkt = cdiv(p.Sk, 128);
-  const int64_t gk = (int64_t)p.nkt * p.B * p.Hkv;
-  if (causal)
-    hipLaunchKernelGGL((dkdv_kernel<T, DT, true>), dim3((unsigned)gk), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL((dkdv_kernel<T, DT, false>), dim3((unsigned)gk), dim3(256), 0, stream, p);
-  return check_launch("kf_attn_bwd(dkdv)");
+static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) {
+  if (stages & KF_BWD_DELTA) {
+    const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
+    hipLaunchKernelGGL((delta_kernel<T>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, stream, p);
+    int rc = check_launch("kf_attn_bwd(delta)");
+    if (rc) return rc;
+  }
+  if (stages & KF_BWD_DQ) {
+    p.nqt = cdiv(p.Sq, 128);
+    const int64_t gq = (int64_t)p.nqt * p.B * p.Hq;
+    if (causal)
+      hipLaunchKernelGGL((dq_kernel<T, DT, true>), dim3((unsigned)gq), dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((dq_kernel<T, DT, false>), dim3((unsigned)gq), dim3(256), 0, stream, p);
+    int rc = check_launch("kf_attn_bwd(dq)");
+    if (rc) return rc;
+  }
+  if (stages & KF_BWD_DKDV) {
+    p.nqt = cdiv(p.Sq, 64);
+    p.nkt = cdiv(p.Sk, 128);
+    const int64_t gk = (int64_t)p.nkt * p.B * p.Hkv;
+    if (causal)
+      hipLaunchKernelGGL((dkdv_kernel<T, DT, true>), dim3((unsigned)gk), dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((dkdv_kernel<T, DT, false>), dim3((unsigned)gk), dim3(256), 0, stream, p);
+    int rc = check_launch("kf_attn_bwd(dkdv)");
+    if (rc) return rc;
+  }
+  return KF_OK;
 }
 
 template <typename T>
-static int dispatch_bwd(const BwdParams& p, bool causal, hipStream_t stream) {
+static int dispatch_bwd(const BwdParams& p, bool causal, int stages, hipStream_t stream) {
   switch (head_tile(p.D)) {
-    case 32: return launch_bwd<T, 32>(p, causal, stream);
-    case 64: return launch_bwd<T, 64>(p, causal, stream);
-    case 96: return launch_bwd<T, 96>(p, causal, stream);
-    default: return launch_bwd<T, 128>(p, causal, stream);
+    case 32: return launch_bwd<T, 32>(p, causal, stages, stream);
+    case 64: return launch_bwd<T, 64>(p, causal, stages, stream);
+    case 96: return launch_bwd<T, 96>(p, causal, stages, stream);
+    default: return launch_bwd<T, 128>(p, causal, stages, stream);
   }
 }
 
@@ -494,16 +502,18 @@ extern "C" size_t kf_attn_bwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv
   return ((rows * sizeof(float) + 255) / 256) * 256;
 }
 
-extern "C" int kf_attn_bwd(const void* q, const void* k, const void* v, const void* o,
-                           const float* lse, const void* dout, void* dq, void* dk, void* dv,
-                           int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
-                           const int64_t* q_strides, const int64_t* k_strides,
-                           const int64_t* v_strides, const int64_t* o_strides,
-                           const int64_t* do_strides, const int64_t* dq_strides,
-                           const int64_t* dk_strides, const int64_t* dv_strides, float scale,
-                           int causal, int dtype, void* workspace, size_t workspace_bytes,
-                           void* stream) {
+extern "C" int kf_attn_bwd_stages(int stages, const void* q, const void* k, const void* v,
+                                  const void* o, const float* lse, const void* dout, void* dq,
+                                  void* dk, void* dv, int64_t B, int64_t Hq, int64_t Hkv,
+                                  int64_t Sq, int64_t Sk, int64_t D, const int64_t* q_strides,
+                                  const int64_t* k_strides, const int64_t* v_strides,
+                                  const int64_t* o_strides, const int64_t* do_strides,
+                                  const int64_t* dq_strides, const int64_t* dk_strides,
+                                  const int64_t* dv_strides, float scale, int causal, int dtype,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
   const char* what = "kf_attn_bwd";
+  if (stages <= 0 || stages > (KF_BWD_DELTA | KF_BWD_DQ | KF_BWD_DKDV))
+    return set_error(KF_EINVAL, "%s: stages must be a non-empty KF_BWD_* mask", what);
   int rc = check_attn_common(what, B, Hq, Hkv, Sq, Sk, D, dtype);
   if (rc) return rc;
   if ((rc = check_tensor(what, "q", q, q_strides)) || (rc = check_tensor(what, "k", k, k_strides)) ||
@@ -536,6 +546,21 @@ extern "C" int kf_attn_bwd(const void* q, const void* k, const void* v, const vo
   p.scale = scale;
   p.scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  return dtype == KF_F16 ? dispatch_bwd<_Float16>(p, causal != 0, s)
-                         : dispatch_bwd<__bf16>(p, causal != 0, s);
+  return dtype == KF_F16 ? dispatch_bwd<_Float16>(p, causal != 0, stages, s)
+                         : dispatch_bwd<__bf16>(p, causal != 0, stages, s);
+}
+
+extern "C" int kf_attn_bwd(const void* q, const void* k, const void* v, const void* o,
+                           const float* lse, const void* dout, void* dq, void* dk, void* dv,
+                           int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                           const int64_t* q_strides, const int64_t* k_strides,
+                           const int64_t* v_strides, const int64_t* o_strides,
+                           const int64_t* do_strides, const int64_t* dq_strides,
+                           const int64_t* dk_strides, const int64_t* dv_strides, float scale,
+                           int causal, int dtype, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  return kf_attn_bwd_stages(KF_BWD_DELTA | KF_BWD_DQ | KF_BWD_DKDV, q, k, v, o, lse, dout, dq, dk,
+                            dv, B, Hq, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides,
+                            do_strides, dq_strides, dk_strides, dv_strides, scale, causal, dtype,
+                            workspace, workspace_bytes, stream);
 }

@@ -72,7 +72,7 @@ __device__ inline void fwd_map_block(int bid, int nqt, int B, int Hq, int Hkv, i
 }
 
 template <typename T, int DT, int QB, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void fwd_kernel(const FwdParams p) {
+__global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdParams p) {
   constexpr int BM = 4 * QB * 32;
   constexpr int BN = 64;
   constexpr int KSTR = DT + 8;   // 16-byte pad: conflict-free b128 row reads
@@ -95,9 +95,9 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(const FwdParams p) {
   const int q0 = qt * BM;
   const int wq0 = q0 + wave * QB * 32;
 
-  const uint16_t* Qp = p.q + b * p.q_sb + h * p.q_sh;
-  const uint16_t* Kp = p.k + b * p.k_sb + kvh * p.k_sh;
-  const uint16_t* Vp = p.v + b * p.v_sb + kvh * p.v_sh;
+  const auto qr = make_rsrc(p.q + b * p.q_sb + h * p.q_sh, rows_extent(p.Sq, p.q_ss, p.D));
+  const auto kr = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, rows_extent(p.Sk, p.k_ss, p.D));
+  const auto vr = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, rows_extent(p.Sk, p.v_ss, p.D));
 
   u32x4 qf[QB][NKS];
 #pragma unroll
@@ -106,7 +106,8 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(const FwdParams p) {
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       const int d = 16 * ks + 8 * h32;
-      qf[qb][ks] = (row < p.Sq && d < p.D) ? ldg16(Qp + row * p.q_ss + d) : zero_u4();
+      const uint32_t off = (row < p.Sq && d < p.D) ? (uint32_t)(row * p.q_ss + d) * 2u : kOOB;
+      qf[qb][ks] = buf_load16(qr, off);
     }
   }
 
@@ -123,17 +124,29 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(const FwdParams p) {
   const int nkeys = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
   const int ntiles = cdiv(nkeys, BN);
 
+  // Per-thread load slots: chunk c covers (row e / CPR, column e % CPR) of the
+  // tile; the byte offsets only move by BN rows per tile.
+  uint32_t koff[CPT], voff[CPT];
+  int lrow[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int e = tid + 256 * c;
+    const int row = e / CPR, col = e % CPR;
+    lrow[c] = row;
+    const bool colok = col * 8 < p.D;
+    koff[c] = colok ? (uint32_t)(row * p.k_ss + col * 8) * 2u : kOOB;
+    voff[c] = colok ? (uint32_t)(row * p.v_ss + col * 8) * 2u : kOOB;
+  }
+  const uint32_t kstep = (uint32_t)(BN * p.k_ss) * 2u, vstep = (uint32_t)(BN * p.v_ss) * 2u;
+
   u32x4 kreg[CPT], vreg[CPT];
   auto gload = [&](int tile) {
     const int kbase = tile * BN;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-      const int e = tid + 256 * c;
-      const int row = e / CPR, col = e % CPR;
-      const int key = kbase + row;
-      const bool ok = key < p.Sk && col * 8 < p.D;
-      kreg[c] = ok ? ldg16(Kp + key * p.k_ss + col * 8) : zero_u4();
-      vreg[c] = ok ? ldg16(Vp + key * p.v_ss + col * 8) : zero_u4();
+      const bool ok = kbase + lrow[c] < p.Sk;
+      kreg[c] = buf_load16(kr, ok ? koff[c] + (uint32_t)tile * kstep : kOOB);
+      vreg[c] = buf_load16(vr, ok ? voff[c] + (uint32_t)tile * vstep : kOOB);
     }
   };
   auto sstore = [&](int buf) {
@@ -193,16 +206,29 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(const FwdParams p) {
             float x = s[qb][kb][r] * p.scale_log2;
             if (need_mask) {
               const int key = kbase + 32 * kb + 8 * (r >> 2) + 4 * h32 + (r & 3);
-              if (key >= p.Sk || (CAUSAL && key > qrow)) x = kNegInf;
+              x = (key >= p.Sk || (CAUSAL && key > qrow)) ? kNegInf : x;
             }
             s[qb][kb][r] = x;
             mx = fmaxf(mx, x);
           }
         }
         mx = wave_xor32_max(mx);
-        const float m_new = fmaxf(m_i[qb], mx);
-        const float msub = (m_new == kNegInf) ? 0.f : m_new;
-        const float alpha = fast_exp2(m_i[qb] - msub);
+        // Lazy rescale: move the reference max only when a score exceeds it
+        // by more than kRescaleThreshold (O and l are still zero while the
+        // max is -inf, so the first finite max is adopted without rescaling).
+        if (m_i[qb] == kNegInf) {
+          m_i[qb] = mx;
+        } else {
+          const bool grow = mx > m_i[qb] + kRescaleThreshold;
+          if (wave_any(grow)) {
+            const float alpha = grow ? fast_exp2(m_i[qb] - mx) : 1.f;
+            l_i[qb] *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) oacc[qb][db] *= alpha;
+            m_i[qb] = grow ? mx : m_i[qb];
+          }
+        }
+        const float msub = (m_i[qb] == kNegInf) ? 0.f : m_i[qb];
         float rs = 0.f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
@@ -213,10 +239,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(const FwdParams p) {
             rs += e;
           }
         }
-        l_i[qb] = l_i[qb] * alpha + rs;
-        m_i[qb] = m_new;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) oacc[qb][db] *= alpha;
+        l_i[qb] += rs;
 #pragma unroll
         for (int st = 0; st < 4; ++st) pk[qb][st] = pack8<T>(s[qb][st >> 1], 8 * (st & 1));
       }
@@ -279,10 +302,9 @@ static int launch_fwd(const FwdParams& prm, bool causal, hipStream_t stream) {
 
 template <typename T>
 static int dispatch_fwd(const FwdParams& p, bool causal, hipStream_t stream) {
-  // Two query blocks per wave halve the LDS traffic per MFMA; use them when the
-  // grid still fills the chip at least twice.
-  const int64_t tiles256 = (int64_t)cdiv(p.Sq, 256) * p.B * p.Hq;
-  const bool qb2 = tiles256 >= 512;
+  // One 32-row block per wave at two waves per SIMD: while one wave runs its
+  // softmax on the VALU the other keeps the MFMA pipe busy.
+  const bool qb2 = false;
   switch (head_tile(p.D)) {
     case 32: return qb2 ? launch_fwd<T, 32, 2>(p, causal, stream) : launch_fwd<T, 32, 1>(p, causal, stream);
     case 64: return qb2 ? launch_fwd<T, 64, 2>(p, causal, stream) : launch_fwd<T, 64, 1>(p, causal, stream);
@@ -305,6 +327,14 @@ int check_attn_common(const char* what, int64_t B, int64_t Hq, int64_t Hkv, int6
     return set_error(KF_EINVAL, "%s: dtype must be KF_F16 or KF_BF16", what);
   if (Sq > 0x3fffffff || Sk > 0x3fffffff || B * Hq > 0x3fffffff)
     return set_error(KF_EUNSUPPORTED, "%s: sizes exceed the kernels' 32-bit row indexing", what);
+  return KF_OK;
+}
+
+// The kernels address one (batch, head) slice through a 32-bit buffer
+// resource: its byte extent must stay below 2^31.
+int check_extent(const char* what, const char* name, int64_t rows, int64_t stride, int64_t D) {
+  if (rows > 0 && ((rows - 1) * stride + D) * 2 > 0x7fffffffLL)
+    return set_error(KF_EUNSUPPORTED, "%s: one head of %s spans more than 2 GiB", what, name);
   return KF_OK;
 }
 
@@ -336,6 +366,9 @@ extern "C" int kf_attn_fwd(const void* q, const void* k, const void* v, void* o,
     return rc;
   if (lse == nullptr) return set_error(KF_EINVAL, "%s: lse is null", what);
   if (!(scale == scale) || scale - scale != 0.f) return set_error(KF_EINVAL, "%s: scale must be finite", what);
+  if ((rc = check_extent(what, "q", Sq, q_strides[2], D)) || (rc = check_extent(what, "k", Sk, k_strides[2], D)) ||
+      (rc = check_extent(what, "v", Sk, v_strides[2], D)))
+    return rc;
   FwdParams p{};
   p.q = (const uint16_t*)q;
   p.k = (const uint16_t*)k;

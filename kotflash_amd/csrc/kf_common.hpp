@@ -98,6 +98,35 @@ __device__ inline u32x4 zero_u4() {
 }
 
 __device__ inline u32x4 ldg16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Raw buffer loads: a wave-uniform resource (base, byte extent) plus a per-lane
+// byte offset. Offsets at or beyond the extent read as zero, so tails of the
+// key/query range and head-dim padding need no branches: invalid lanes pass
+// kOOB. The extent is limited to 2^31 - 1 bytes (checked on the host).
+constexpr uint32_t kOOB = 0x80000000u;
+
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ inline u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+
+// Byte extent of rows [0, n) of a [rows, D] slice with a row stride of
+// `stride` elements (16-bit): the last row ends at (n - 1) * stride + D.
+__device__ inline uint32_t rows_extent(int n, int64_t stride, int D) {
+  return n > 0 ? (uint32_t)((((int64_t)(n - 1)) * stride + D) * 2) : 0u;
+}
+
+// Wave-uniform "any lane" for a per-lane predicate.
+__device__ inline bool wave_any(bool pred) { return __builtin_amdgcn_ballot_w64(pred) != 0; }
+
+// Lazy rescaling threshold of the online softmax (log2 units): the reference
+// max m of a row is only moved (and O, l rescaled) when a new score exceeds it
+// by more than this, so P = 2^(s - m) stays <= 2^8 -- exact in fp32 and
+// representable in fp16/bf16 -- and most tiles skip the O rescale entirely.
+constexpr float kRescaleThreshold = 8.f;
 __device__ inline void stg16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 __device__ inline u32x4 lds_read16(const uint16_t* p) {

@@ -51,7 +51,7 @@ def _decode(q, k, v, seqlens: Optional[torch.Tensor], scale: float, with_lse: bo
     out = torch.empty((b, hq, sq, d), device=q.device, dtype=q.dtype)
     lse = torch.empty((b, hq, sq), device=q.device, dtype=torch.float32) if with_lse else None
     splits = _hip.decode_num_splits(b, hq, hkv, sq, sk, d)
-    nbytes = _hip.decode_workspace_bytes(b, hq, sq, d, splits)
+    nbytes = _hip.decode_workspace_bytes(b, hq, hkv, sq, d, splits)
     ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8) if nbytes else None
     _hip.decode(q, k, v, out, lse, seqlens, scale=scale, num_splits=splits, workspace=ws)
     return out, lse

@@ -57,7 +57,7 @@ def attention_forward(q, k, v, *, causal: bool, scale: float):
     lse = torch.empty((b, hq, sq), device=q.device, dtype=torch.float32)
     if gfx950_decode_eligible(sq, sk, dp, causal=causal):
         splits = _hip.decode_num_splits(b, hq, hkv, sq, sk, dp)
-        nbytes = _hip.decode_workspace_bytes(b, hq, sq, dp, splits)
+        nbytes = _hip.decode_workspace_bytes(b, hq, hkv, sq, dp, splits)
         ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8) if nbytes else None
         _hip.decode(q_, k_, v_, out, lse, None, scale=scale, num_splits=splits, workspace=ws)
     else:

@@ -88,17 +88,17 @@ def test_decode_planner_and_workspace():
     lib = _hip.lib()
     for sk in (2048, 4096, 8192, 16384, 1537, 8193, 100000):
         ns = lib.kf_decode_num_splits(2, 8, 2, 1, sk, 64)
-        chunk = ((-(-sk // ns)) + 127) // 128 * 128
+        chunk = ((-(-sk // ns)) + 255) // 256 * 256
         assert ns >= 1 and -(-sk // chunk) == ns
-    assert lib.kf_decode_num_splits(2, 8, 2, 1, 16384, 64) == 128
-    assert lib.kf_decode_workspace_bytes(2, 8, 1, 64, 1) == 0
-    assert lib.kf_decode_workspace_bytes(2, 8, 1, 64, 128) >= 128 * 16 * 65 * 4
+    assert lib.kf_decode_num_splits(2, 8, 2, 1, 16384, 64) == 64
+    assert lib.kf_decode_workspace_bytes(2, 8, 2, 1, 64, 1) == 0
+    assert lib.kf_decode_workspace_bytes(2, 8, 2, 1, 64, 128) >= 128 * 16 * 65 * 4
     s = _arr(512, 64, 64)
     rc = lib.kf_attn_decode(0x1000, 0x2000, 0x3000, 0x4000, None, None, 2, 8, 2, 1, 16384, 64,
                             s, s, s, s, 0.125, 127, 0, None, 0, None)
     assert rc == 1 and "partition" in lib.kf_last_error().decode()
     rc = lib.kf_attn_decode(0x1000, 0x2000, 0x3000, 0x4000, None, None, 2, 8, 2, 1, 16384, 64,
-                            s, s, s, s, 0.125, 128, 0, None, 0, None)
+                            s, s, s, s, 0.125, 64, 0, None, 0, None)
     assert rc == 1 and "workspace" in lib.kf_last_error().decode()
 
 
