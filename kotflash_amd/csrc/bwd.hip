@@ -1,19 +1,28 @@
 // Attention backward for gfx950.
 //
-// Three launches on one stream, no atomics, deterministic:
+// Launches on one stream, no atomics, deterministic:
 //   1. delta_kernel: delta[i] = sum_d O[i,d] * dO[i,d] from the stored
 //      low-precision O (reference triton_backward.py:45).
-//   2. dq_kernel (query-stationary, same layout as the forward): per key tile it
-//      recomputes S^T = K Q^T and dP^T = V dO^T, forms
+//   2. dq_kernel (query-stationary, same layout as the forward, two waves per
+//      SIMD): per key tile it recomputes S^T = K Q^T and dP^T = V dO^T, forms
 //      dS^T = P^T (dP^T - delta) with P = exp(scale S - LSE), and accumulates
-//      dQ^T += K^T dS^T; dQ = scale * dQ^T^T  (reference :17-91).
-//   3. dkdv_kernel (key-stationary): a workgroup owns 128 keys of one
-//      (batch, kv_head); K and V stay in registers as MFMA B operands, and for
-//      every query head of the GQA group and every query tile it recomputes
-//      S = Q K^T and dP = dO V^T, then accumulates dV^T += dO^T P and
-//      dK^T += Q^T dS in registers. The group sum over query heads therefore
-//      happens in registers, without partial buffers (reference :94-195, where
-//      the group loop is :136-137 and the products :183-184).
+//      dQ^T += K^T dS^T; dQ = scale * dQ (reference :17-91).
+//   3. dkdv_kernel (key-stationary, 8 waves per workgroup): a key tile is 128
+//      keys of one (batch, kv_head) held in LDS; for every query head of the
+//      GQA group and every 64-row query tile the kernel recomputes S = Q K^T
+//      and dP = dO V^T and accumulates dV^T += dO^T P and dK^T += Q^T dS in
+//      registers (wave w owns keys 32 (w % 4) .. +31 and query rows
+//      32 (w / 4) .. +31 of each tile; the two query halves are summed in LDS
+//      when the tile is done). The group sum over query heads therefore happens
+//      in registers (reference :94-195, group loop :136-137, products
+//      :183-184). Work is split stream-K style: the (key tile, head, query tile)
+//      units of all tiles are laid end to end and every workgroup takes an
+//      equal share, so causal tiles of very different sizes still keep every
+//      CU busy until the end. A tile shared by several workgroups is written
+//      as fp32 partials and
+//   4. dkdv_fixup_kernel sums those partials (and zero-fills keys that no query
+//      can see); the reference instead splits long query ranges into a fixed
+//      number of fp32 partial copies plus a reduction pass (:198-332).
 // P and dS are rounded to the input dtype before the products that consume
 // them, as in the reference (:85, :183-184).
 #include "kf_common.hpp"
@@ -24,6 +33,7 @@ namespace kf {
 int check_attn_common(const char* what, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk,
                       int64_t D, int dtype);
 int check_tensor(const char* what, const char* name, const void* ptr, const int64_t* strides);
+int check_extent(const char* what, const char* name, int64_t rows, int64_t stride, int64_t D);
 
 struct BwdParams {
   const uint16_t* q;
@@ -33,6 +43,7 @@ struct BwdParams {
   const uint16_t* dout;
   const float* lse;
   float* delta;
+  float* part;  // dK/dV fp32 partials: [2 * nwg][2][128][DT]
   uint16_t* dq;
   uint16_t* dk;
   uint16_t* dv;
@@ -45,9 +56,31 @@ struct BwdParams {
   int64_t dk_sb, dk_sh, dk_ss;
   int64_t dv_sb, dv_sh, dv_ss;
   int B, Hq, Hkv, Sq, Sk, D;
-  int nqt, nkt;
+  int G, ngroups;
+  int nqt, nkt;    // dq: 128-row query tiles; dkdv: 64-row query tiles, 128-key tiles
+  int nwg;         // dkdv workgroups (stream-K share count)
+  int64_t units;   // dkdv: total (key tile, head, query tile) units
   float scale, scale_log2;
 };
+
+// Key-stationary tiling shared by dkdv_kernel, the fixup and the host.
+constexpr int kBNK = 128;  // keys per tile
+constexpr int kBMQ = 64;   // query rows per unit
+
+__host__ __device__ inline int dkdv_qstart(int kt, bool causal) {
+  // Under the upper-left causal mask, query i sees key j iff j <= i, so no
+  // query before the tile's first key (kt * 128) contributes.
+  return causal ? kt * (kBNK / kBMQ) : 0;
+}
+__host__ __device__ inline int dkdv_nq(int kt, int nqt, bool causal) {
+  const int n = nqt - dkdv_qstart(kt, causal);
+  return n > 0 ? n : 0;
+}
+// Workgroup w owns units [floor(w U / N), floor((w + 1) U / N)).
+__host__ __device__ inline int64_t dkdv_u0(int64_t w, int64_t U, int64_t N) { return w * U / N; }
+__host__ __device__ inline int64_t dkdv_owner(int64_t u, int64_t U, int64_t N) {
+  return ((u + 1) * N + U - 1) / U - 1;
+}
 
 // ---------------------------------------------------------------------------
 // 1. delta = rowsum(O * dO): 16 lanes per row, 16 rows per workgroup.
@@ -81,9 +114,11 @@ __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. dQ, query-stationary. QB = 1 block of 32 rows per wave, BM = 128.
+// 2. dQ, query-stationary: 4 waves x 32 rows, 64-key tiles, two workgroups
+// per CU. Each 32-key block is finished (S, dP, dS, dQ update) before the next
+// starts so the live registers fit two waves per SIMD.
 template <typename T, int DT, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void dq_kernel(const BwdParams p) {
+__global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
   constexpr int BM = 128;
   constexpr int BN = 64;
   constexpr int KSTR = DT + 16;  // K: b128 reads for S^T and transposed reads for dQ^T
@@ -100,18 +135,17 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdParams p) {
   const int lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, h32 = lane >> 5;
 
-  // Longest query tiles first; same XCD grouping as the forward.
+  // Longest query tiles first; KV groups kept on one XCD as in the forward.
   int qt, b, h;
   {
-    const int G = p.Hq / p.Hkv, ngroups = p.B * p.Hkv;
     const int bid = blockIdx.x;
-    if ((ngroups & 7) == 0) {
-      const int x = bid & 7, j = bid >> 3, gpx = ngroups >> 3, per_tile = G * gpx;
+    if ((p.ngroups & 7) == 0) {
+      const int x = bid & 7, j = bid >> 3, gpx = p.ngroups >> 3, per_tile = p.G * gpx;
       const int t = j / per_tile, r = j - t * per_tile;
       qt = p.nqt - 1 - t;
-      const int grp = x + 8 * (r / G);
+      const int grp = x + 8 * (r / p.G);
       b = grp / p.Hkv;
-      h = (grp % p.Hkv) * G + r % G;
+      h = (grp % p.Hkv) * p.G + r % p.G;
     } else {
       const int bh = p.B * p.Hq, t = bid / bh, r = bid - t * bh;
       qt = p.nqt - 1 - t;
@@ -119,23 +153,23 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdParams p) {
       h = r % p.Hq;
     }
   }
-  const int kvh = h / (p.Hq / p.Hkv);
+  const int kvh = h / p.G;
   const int q0 = qt * BM;
   const int qrow = q0 + wave * 32 + l32;
   const bool row_ok = qrow < p.Sq;
 
-  const uint16_t* Qp = p.q + b * p.q_sb + h * p.q_sh;
-  const uint16_t* DOp = p.dout + b * p.do_sb + h * p.do_sh;
-  const uint16_t* Kp = p.k + b * p.k_sb + kvh * p.k_sh;
-  const uint16_t* Vp = p.v + b * p.v_sb + kvh * p.v_sh;
+  const auto qr = make_rsrc(p.q + b * p.q_sb + h * p.q_sh, rows_extent(p.Sq, p.q_ss, p.D));
+  const auto dor = make_rsrc(p.dout + b * p.do_sb + h * p.do_sh, rows_extent(p.Sq, p.do_ss, p.D));
+  const auto kr = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, rows_extent(p.Sk, p.k_ss, p.D));
+  const auto vr = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, rows_extent(p.Sk, p.v_ss, p.D));
 
   u32x4 qf[NKS], dof[NKS];
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) {
     const int d = 16 * ks + 8 * h32;
     const bool ok = row_ok && d < p.D;
-    qf[ks] = ok ? ldg16(Qp + qrow * p.q_ss + d) : zero_u4();
-    dof[ks] = ok ? ldg16(DOp + qrow * p.do_ss + d) : zero_u4();
+    qf[ks] = buf_load16(qr, ok ? (uint32_t)(qrow * p.q_ss + d) * 2u : kOOB);
+    dof[ks] = buf_load16(dor, ok ? (uint32_t)(qrow * p.do_ss + d) * 2u : kOOB);
   }
   const int64_t rowlin = ((int64_t)b * p.Hq + h) * p.Sq + qrow;
   const float lse2 = row_ok ? p.lse[rowlin] * kLog2e : 0.f;
@@ -157,8 +191,8 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdParams p) {
       const int row = e / CPR, col = e % CPR;
       const int key = kbase + row;
       const bool ok = key < p.Sk && col * 8 < p.D;
-      kreg[c] = ok ? ldg16(Kp + key * p.k_ss + col * 8) : zero_u4();
-      vreg[c] = ok ? ldg16(Vp + key * p.v_ss + col * 8) : zero_u4();
+      kreg[c] = buf_load16(kr, ok ? (uint32_t)(key * p.k_ss + col * 8) * 2u : kOOB);
+      vreg[c] = buf_load16(vr, ok ? (uint32_t)(key * p.v_ss + col * 8) * 2u : kOOB);
     }
   };
   auto sstore = [&](int buf) {
@@ -186,44 +220,36 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdParams p) {
     const uint16_t* Ks = smem + buf * STAGE;
     const uint16_t* Vs = Ks + KT;
     const int kbase = it * BN;
-    const bool active = !CAUSAL || kbase <= wq0 + 31;
-    if (active) {
-      f32x16 s[2], dp[2];
-      s[0] = zero16(); s[1] = zero16(); dp[0] = zero16(); dp[1] = zero16();
+    const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && kbase + BN - 1 > wq0);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb) {
+      const int kb0 = kbase + 32 * kb;
+      if (CAUSAL && kb0 > wq0 + 31) continue;  // block entirely above the wave's rows
+      f32x16 s = zero16(), dp = zero16();
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const u32x4 a = lds_read16(Ks + (kb * 32 + l32) * KSTR + 16 * ks + 8 * h32);
-          s[kb] = Elem<T>::mfma(a, qf[ks], s[kb]);
-          const u32x4 a2 = lds_read16(Vs + (kb * 32 + l32) * VSTR + 16 * ks + 8 * h32);
-          dp[kb] = Elem<T>::mfma(a2, dof[ks], dp[kb]);
-        }
+      for (int ks = 0; ks < NKS; ++ks) {
+        const u32x4 a = lds_read16(Ks + (kb * 32 + l32) * KSTR + 16 * ks + 8 * h32);
+        s = Elem<T>::mfma(a, qf[ks], s);
+        const u32x4 a2 = lds_read16(Vs + (kb * 32 + l32) * VSTR + 16 * ks + 8 * h32);
+        dp = Elem<T>::mfma(a2, dof[ks], dp);
       }
-      const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && kbase + BN - 1 > wq0);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          bool valid = true;
-          if (need_mask) {
-            const int key = kbase + 32 * kb + 8 * (r >> 2) + 4 * h32 + (r & 3);
-            valid = key < p.Sk && (!CAUSAL || key <= qrow);
-          }
-          const float pv = valid ? fast_exp2(s[kb][r] * p.scale_log2 - lse2) : 0.f;
-          dp[kb][r] = pv * (dp[kb][r] - dlt);
+      for (int r = 0; r < 16; ++r) {
+        bool valid = true;
+        if (need_mask) {
+          const int key = kb0 + 8 * (r >> 2) + 4 * h32 + (r & 3);
+          valid = key < p.Sk && (!CAUSAL || key <= qrow);
         }
+        const float pv = valid ? fast_exp2(s[r] * p.scale_log2 - lse2) : 0.f;
+        dp[r] = pv * (dp[r] - dlt);
       }
-      u32x4 dsk[4];
-#pragma unroll
-      for (int st = 0; st < 4; ++st) dsk[st] = pack8<T>(dp[st >> 1], 8 * (st & 1));
+      const u32x4 ds0 = pack8<T>(dp, 0), ds1 = pack8<T>(dp, 8);
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          const u32x4 a = lds_read_tr_operand(Ks, KSTR, 16 * st, 32 * db, lane);
-          dq[db] = Elem<T>::mfma(a, dsk[st], dq[db]);
-        }
+        const u32x4 a = lds_read_tr_operand(Ks, KSTR, 32 * kb, 32 * db, lane);
+        dq[db] = Elem<T>::mfma(a, ds0, dq[db]);
+        const u32x4 a2 = lds_read_tr_operand(Ks, KSTR, 32 * kb + 16, 32 * db, lane);
+        dq[db] = Elem<T>::mfma(a2, ds1, dq[db]);
       }
     }
     if (it + 1 < ntiles) sstore(buf ^ 1);
@@ -249,146 +275,155 @@ __global__ __launch_bounds__(256, 1) void dq_kernel(const BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// 3. dK/dV, key-stationary. 4 waves x 32 keys = 128 keys per workgroup, query
-// tiles of 64 rows.
+// 3. dK/dV, key-stationary, stream-K over (key tile, head, query tile) units.
 template <typename T, int DT, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
-  constexpr int BNK = 128;
-  constexpr int BMQ = 64;
-  constexpr int QSTR = DT + 16;  // b128 row reads and transposed reads
-  constexpr int QT = BMQ * QSTR;
-  constexpr int STAGE = 2 * QT;  // Q tile, dO tile
+__global__ __launch_bounds__(512, 1) void dkdv_kernel(const BwdParams p) {
+  constexpr int KSTR = DT + 8;   // K/V tiles: b128 reads
+  constexpr int QSTR = DT + 16;  // Q/dO tiles: b128 and transposed reads
+  constexpr int KVT = kBNK * KSTR;
+  constexpr int QT = kBMQ * QSTR;
   constexpr int CPR = DT / 8;
-  constexpr int CPT = BMQ * CPR / 256;
+  constexpr int QCH = kBMQ * CPR;          // 16-byte chunks of a Q (or dO) tile
+  constexpr int QCPT = (QCH + 511) / 512;  // per thread
+  constexpr int KVCPT = kBNK * CPR / 512;  // K (or V) tile chunks per thread
   constexpr int NKS = DT / 16;
   constexpr int NDB = DT / 32;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
-  __shared__ __attribute__((aligned(16))) float rowstat[2][2][BMQ];  // [buf][lse2, delta][row]
+  constexpr int RSTR = DT + 1;             // padded rows of the flush reduction
+  static_assert(kBNK * RSTR * 4 <= 2 * QT * 2 * 2, "flush reduction must fit the Q/dO stages");
+  static_assert(kBNK * RSTR * 4 <= 2 * KVT * 2, "flush reduction must fit the K/V tiles");
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * KVT + 4 * QT];
+  __shared__ __attribute__((aligned(16))) float rowstat[2][2][kBMQ];  // [buf][lse2, delta][row]
+  uint16_t* const Ks = smem;
+  uint16_t* const Vs = smem + KVT;
+  uint16_t* const Qstage = smem + 2 * KVT;  // [buf][Q | dO]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, h32 = lane >> 5;
-  const int G = p.Hq / p.Hkv;
+  const int kbw = wave & 3, qh = wave >> 2;
 
-  // Key tile 0 has the most causal work: issue key tiles in ascending order,
-  // KV groups on XCDs as in the forward.
-  int kt, b, kvh;
-  {
-    const int ngroups = p.B * p.Hkv, bid = blockIdx.x;
-    int grp;
-    if ((ngroups & 7) == 0) {
-      const int x = bid & 7, j = bid >> 3, gpx = ngroups >> 3;
-      kt = j / gpx;
-      grp = x + 8 * (j % gpx);
-    } else {
-      kt = bid / ngroups;
-      grp = bid % ngroups;
-    }
-    b = grp / p.Hkv;
-    kvh = grp % p.Hkv;
-  }
-  const int k0 = kt * BNK;
-  const int kw0 = k0 + wave * 32;
-  const int key = kw0 + l32;
-  const bool key_ok = key < p.Sk;
+  const int64_t N = gridDim.x;
+  int64_t u = dkdv_u0(blockIdx.x, p.units, N);
+  const int64_t uend = dkdv_u0(blockIdx.x + 1, p.units, N);
+  if (u >= uend) return;
 
-  const uint16_t* Kp = p.k + b * p.k_sb + kvh * p.k_sh;
-  const uint16_t* Vp = p.v + b * p.v_sb + kvh * p.v_sh;
-  u32x4 kf[NKS], vf[NKS];
-#pragma unroll
-  for (int ks = 0; ks < NKS; ++ks) {
-    const int d = 16 * ks + 8 * h32;
-    const bool ok = key_ok && d < p.D;
-    kf[ks] = ok ? ldg16(Kp + key * p.k_ss + d) : zero_u4();
-    vf[ks] = ok ? ldg16(Vp + key * p.v_ss + d) : zero_u4();
-  }
   f32x16 dk[NDB], dv[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-    dk[db] = zero16();
-    dv[db] = zero16();
-  }
-
-  // Query tiles that can see any key of this workgroup.
-  const int qt_start = CAUSAL ? (k0 / BMQ) : 0;
-  const int nq = max(0, p.nqt - qt_start);
-  const int niter = G * nq;
-
-  u32x4 qreg[CPT], dreg[CPT];
+  u32x4 qreg[QCPT], dreg[QCPT];
   float st_l = 0.f, st_d = 0.f;
-  auto gload = [&](int it) {
-    const int g = it / nq;
-    const int qt = qt_start + (it - g * nq);
-    const int h = kvh * G + g;
-    const int qbase = qt * BMQ;
-    const uint16_t* Qp = p.q + b * p.q_sb + h * p.q_sh;
-    const uint16_t* DOp = p.dout + b * p.do_sb + h * p.do_sh;
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int e = tid + 256 * c;
-      const int row = e / CPR, col = e % CPR;
-      const int qi = qbase + row;
-      const bool ok = qi < p.Sq && col * 8 < p.D;
-      qreg[c] = ok ? ldg16(Qp + qi * p.q_ss + col * 8) : zero_u4();
-      dreg[c] = ok ? ldg16(DOp + qi * p.do_ss + col * 8) : zero_u4();
-    }
-    if (tid < BMQ) {
-      const int qi = qbase + tid;
-      const int64_t rl = ((int64_t)b * p.Hq + h) * p.Sq + qi;
-      st_l = qi < p.Sq ? p.lse[rl] * kLog2e : 0.f;
-      st_d = qi < p.Sq ? p.delta[rl] : 0.f;
-    }
-  };
-  auto sstore = [&](int buf) {
-    uint16_t* Qs = smem + buf * STAGE;
-    uint16_t* Ds = Qs + QT;
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int e = tid + 256 * c;
-      const int row = e / CPR, col = e % CPR;
-      lds_write16(Qs + row * QSTR + col * 8, qreg[c]);
-      lds_write16(Ds + row * QSTR + col * 8, dreg[c]);
-    }
-    if (tid < BMQ) {
-      rowstat[buf][0][tid] = st_l;
-      rowstat[buf][1][tid] = st_d;
-    }
-  };
 
-  if (niter > 0) {
-    gload(0);
-    sstore(0);
-  }
-  __syncthreads();
+  int kt = 0;
+  int64_t row_base = 0;  // first unit of key-tile row kt
+  bool first_seg = true;
+  while (u < uend) {
+    for (;;) {
+      const int64_t row_units = (int64_t)p.ngroups * p.G * dkdv_nq(kt, p.nqt, CAUSAL);
+      if (u < row_base + row_units) break;
+      row_base += row_units;
+      ++kt;
+    }
+    const int nq = dkdv_nq(kt, p.nqt, CAUSAL);
+    const int qs = dkdv_qstart(kt, CAUSAL);
+    const int per_tile = p.G * nq;
+    const int64_t off = u - row_base;
+    const int grp = (int)(off / per_tile);
+    const int ua = (int)(off % per_tile);
+    const int ub = (int)min((int64_t)per_tile, ua + (uend - u));
+    const int b = grp / p.Hkv, kvh = grp % p.Hkv;
+    const int k0 = kt * kBNK;
 
-  for (int it = 0; it < niter; ++it) {
-    const int buf = it & 1;
-    if (it + 1 < niter) gload(it + 1);
-    const int g = it / nq;
-    const int qt = qt_start + (it - g * nq);
-    const int qbase = qt * BMQ;
-    const uint16_t* Qs = smem + buf * STAGE;
-    const uint16_t* Ds = Qs + QT;
-    const bool active = !CAUSAL || qbase + BMQ - 1 >= kw0;
-    if (active) {
-      f32x16 s[2], dp[2];
-      s[0] = zero16(); s[1] = zero16(); dp[0] = zero16(); dp[1] = zero16();
+    __syncthreads();  // previous segment's flush has finished with LDS
+    {
+      const auto kr = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, rows_extent(p.Sk, p.k_ss, p.D));
+      const auto vr = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, rows_extent(p.Sk, p.v_ss, p.D));
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
+      for (int c = 0; c < KVCPT; ++c) {
+        const int e = tid + 512 * c;
+        const int row = e / CPR, col = e % CPR;
+        const int key = k0 + row;
+        const bool ok = key < p.Sk && col * 8 < p.D;
+        const u32x4 kk = buf_load16(kr, ok ? (uint32_t)(key * p.k_ss + col * 8) * 2u : kOOB);
+        const u32x4 vv = buf_load16(vr, ok ? (uint32_t)(key * p.v_ss + col * 8) * 2u : kOOB);
+        lds_write16(Ks + row * KSTR + col * 8, kk);
+        lds_write16(Vs + row * KSTR + col * 8, vv);
+      }
+    }
 #pragma unroll
-        for (int qq = 0; qq < 2; ++qq) {
-          const u32x4 a = lds_read16(Qs + (qq * 32 + l32) * QSTR + 16 * ks + 8 * h32);
-          s[qq] = Elem<T>::mfma(a, kf[ks], s[qq]);
-          const u32x4 a2 = lds_read16(Ds + (qq * 32 + l32) * QSTR + 16 * ks + 8 * h32);
-          dp[qq] = Elem<T>::mfma(a2, vf[ks], dp[qq]);
+    for (int db = 0; db < NDB; ++db) {
+      dk[db] = zero16();
+      dv[db] = zero16();
+    }
+
+    auto gload = [&](int it) {
+      const int g = it / nq;
+      const int qt = qs + (it - g * nq);
+      const int h = kvh * p.G + g;
+      const int qbase = qt * kBMQ;
+      const auto qr = make_rsrc(p.q + b * p.q_sb + h * p.q_sh, rows_extent(p.Sq, p.q_ss, p.D));
+      const auto dor = make_rsrc(p.dout + b * p.do_sb + h * p.do_sh, rows_extent(p.Sq, p.do_ss, p.D));
+#pragma unroll
+      for (int c = 0; c < QCPT; ++c) {
+        const int e = tid + 512 * c;
+        const int row = e / CPR, col = e % CPR;
+        const int qi = qbase + row;
+        const bool ok = e < QCH && qi < p.Sq && col * 8 < p.D;
+        qreg[c] = buf_load16(qr, ok ? (uint32_t)(qi * p.q_ss + col * 8) * 2u : kOOB);
+        dreg[c] = buf_load16(dor, ok ? (uint32_t)(qi * p.do_ss + col * 8) * 2u : kOOB);
+      }
+      if (tid < kBMQ) {
+        const int qi = qbase + tid;
+        const int64_t rl = ((int64_t)b * p.Hq + h) * p.Sq + qi;
+        st_l = qi < p.Sq ? p.lse[rl] * kLog2e : 0.f;
+        st_d = qi < p.Sq ? p.delta[rl] : 0.f;
+      }
+    };
+    auto sstore = [&](int buf) {
+      uint16_t* Qs = Qstage + buf * 2 * QT;
+      uint16_t* Ds = Qs + QT;
+#pragma unroll
+      for (int c = 0; c < QCPT; ++c) {
+        const int e = tid + 512 * c;
+        if (e < QCH) {
+          const int row = e / CPR, col = e % CPR;
+          lds_write16(Qs + row * QSTR + col * 8, qreg[c]);
+          lds_write16(Ds + row * QSTR + col * 8, dreg[c]);
         }
       }
-      const bool need_mask = (qbase + BMQ > p.Sq) || !key_ok || (CAUSAL && qbase < kw0 + 31);
+      if (tid < kBMQ) {
+        rowstat[buf][0][tid] = st_l;
+        rowstat[buf][1][tid] = st_d;
+      }
+    };
+
+    const int key = k0 + kbw * 32 + l32;
+    const bool key_ok = key < p.Sk;
+    gload(ua);
+    sstore(0);
+    __syncthreads();
+    for (int it = ua; it < ub; ++it) {
+      const int buf = (it - ua) & 1;
+      if (it + 1 < ub) gload(it + 1);
+      const int g = it / nq;
+      const int qt = qs + (it - g * nq);
+      const int qw0 = qt * kBMQ + qh * 32;  // first query row of this wave
+      const uint16_t* Qs = Qstage + buf * 2 * QT;
+      const uint16_t* Ds = Qs + QT;
+      const bool active = !CAUSAL || qw0 + 31 >= k0 + kbw * 32;
+      if (active) {
+        f32x16 s = zero16(), dp = zero16();
 #pragma unroll
-      for (int qq = 0; qq < 2; ++qq) {
+        for (int ks = 0; ks < NKS; ++ks) {
+          const u32x4 aq = lds_read16(Qs + (qh * 32 + l32) * QSTR + 16 * ks + 8 * h32);
+          const u32x4 bk = lds_read16(Ks + (kbw * 32 + l32) * KSTR + 16 * ks + 8 * h32);
+          s = Elem<T>::mfma(aq, bk, s);
+          const u32x4 ad = lds_read16(Ds + (qh * 32 + l32) * QSTR + 16 * ks + 8 * h32);
+          const u32x4 bv = lds_read16(Vs + (kbw * 32 + l32) * KSTR + 16 * ks + 8 * h32);
+          dp = Elem<T>::mfma(ad, bv, dp);
+        }
+        // S layout: lane = key, register r = query row 8 (r/4) + 4 h + r % 4.
+        const bool need_mask = (qw0 + 32 > p.Sq) || !key_ok || (CAUSAL && qw0 < k0 + kbw * 32 + 31);
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
-          const int rl = qq * 32 + 8 * g4 + 4 * h32;
+          const int rl = qh * 32 + 8 * g4 + 4 * h32;
           const f32x4 l4 = *reinterpret_cast<const f32x4*>(&rowstat[buf][0][rl]);
           const f32x4 d4 = *reinterpret_cast<const f32x4*>(&rowstat[buf][1][rl]);
 #pragma unroll
@@ -396,57 +431,162 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
             const int r = 4 * g4 + e;
             bool valid = true;
             if (need_mask) {
-              const int qi = qbase + rl + e;
+              const int qi = qw0 + 8 * g4 + 4 * h32 + e;
               valid = qi < p.Sq && key_ok && (!CAUSAL || key <= qi);
             }
-            const float pv = valid ? fast_exp2(s[qq][r] * p.scale_log2 - l4[e]) : 0.f;
-            s[qq][r] = pv;
-            dp[qq][r] = pv * (dp[qq][r] - d4[e]);
+            const float pv = valid ? fast_exp2(s[r] * p.scale_log2 - l4[e]) : 0.f;
+            s[r] = pv;
+            dp[r] = pv * (dp[r] - d4[e]);
           }
         }
-      }
-      u32x4 pk[4], dsk[4];
+        const u32x4 p0 = pack8<T>(s, 0), p1 = pack8<T>(s, 8);
+        const u32x4 s0 = pack8<T>(dp, 0), s1 = pack8<T>(dp, 8);
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        pk[st] = pack8<T>(s[st >> 1], 8 * (st & 1));
-        dsk[st] = pack8<T>(dp[st >> 1], 8 * (st & 1));
+        for (int db = 0; db < NDB; ++db) {
+          u32x4 a = lds_read_tr_operand(Ds, QSTR, qh * 32, 32 * db, lane);
+          dv[db] = Elem<T>::mfma(a, p0, dv[db]);
+          a = lds_read_tr_operand(Ds, QSTR, qh * 32 + 16, 32 * db, lane);
+          dv[db] = Elem<T>::mfma(a, p1, dv[db]);
+          a = lds_read_tr_operand(Qs, QSTR, qh * 32, 32 * db, lane);
+          dk[db] = Elem<T>::mfma(a, s0, dk[db]);
+          a = lds_read_tr_operand(Qs, QSTR, qh * 32 + 16, 32 * db, lane);
+          dk[db] = Elem<T>::mfma(a, s1, dk[db]);
+        }
       }
+      if (it + 1 < ub) sstore(buf ^ 1);
+      __syncthreads();
+    }
+
+    // Flush: waves of query half 1 hand their sums to half 0 through LDS
+    // (dK in the Q/dO stages, dV in the K/V tiles), which stores the tile.
+    float* rk = reinterpret_cast<float*>(Qstage);
+    float* rv = reinterpret_cast<float*>(smem);
+    if (qh == 1) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          const u32x4 a = lds_read_tr_operand(Ds, QSTR, 16 * st, 32 * db, lane);
-          dv[db] = Elem<T>::mfma(a, pk[st], dv[db]);
-          const u32x4 a2 = lds_read_tr_operand(Qs, QSTR, 16 * st, 32 * db, lane);
-          dk[db] = Elem<T>::mfma(a2, dsk[st], dk[db]);
+        for (int r = 0; r < 16; ++r) {
+          const int d = 32 * db + 8 * (r >> 2) + 4 * h32 + (r & 3);
+          rk[(kbw * 32 + l32) * RSTR + d] = dk[db][r];
+          rv[(kbw * 32 + l32) * RSTR + d] = dv[db][r];
         }
       }
     }
-    if (it + 1 < niter) sstore(buf ^ 1);
     __syncthreads();
-  }
-
-  if (key_ok) {
-    uint16_t* Dk = p.dk + b * p.dk_sb + kvh * p.dk_sh + key * p.dk_ss;
-    uint16_t* Dv = p.dv + b * p.dv_sb + kvh * p.dv_sh + key * p.dv_ss;
+    if (qh == 0) {
+      const bool full = ua == 0 && ub == per_tile;
+      float* slot = p.part + (int64_t)(2 * blockIdx.x + (first_seg ? 0 : 1)) * 2 * kBNK * DT;
+      uint16_t* Dk = p.dk + b * p.dk_sb + kvh * p.dk_sh + key * p.dk_ss;
+      uint16_t* Dv = p.dv + b * p.dv_sb + kvh * p.dv_sh + key * p.dv_ss;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
+      for (int db = 0; db < NDB; ++db) {
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d = 32 * db + 8 * g4 + 4 * h32;
-        if (d < p.D) {
-          u32x2 w;
-          w[0] = pack2<T>(dk[db][4 * g4 + 0] * p.scale, dk[db][4 * g4 + 1] * p.scale);
-          w[1] = pack2<T>(dk[db][4 * g4 + 2] * p.scale, dk[db][4 * g4 + 3] * p.scale);
-          *reinterpret_cast<u32x2*>(Dk + d) = w;
-          u32x2 w2;
-          w2[0] = pack2<T>(dv[db][4 * g4 + 0], dv[db][4 * g4 + 1]);
-          w2[1] = pack2<T>(dv[db][4 * g4 + 2], dv[db][4 * g4 + 3]);
-          *reinterpret_cast<u32x2*>(Dv + d) = w2;
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d = 32 * db + 8 * g4 + 4 * h32;
+          float kk[4], vv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            kk[e] = (dk[db][4 * g4 + e] + rk[(kbw * 32 + l32) * RSTR + d + e]) * p.scale;
+            vv[e] = dv[db][4 * g4 + e] + rv[(kbw * 32 + l32) * RSTR + d + e];
+          }
+          if (full) {
+            if (key_ok && d < p.D) {
+              u32x2 w;
+              w[0] = pack2<T>(kk[0], kk[1]);
+              w[1] = pack2<T>(kk[2], kk[3]);
+              *reinterpret_cast<u32x2*>(Dk + d) = w;
+              w[0] = pack2<T>(vv[0], vv[1]);
+              w[1] = pack2<T>(vv[2], vv[3]);
+              *reinterpret_cast<u32x2*>(Dv + d) = w;
+            }
+          } else {
+            float* sk = slot + (kbw * 32 + l32) * DT + d;
+            *reinterpret_cast<float4*>(sk) = make_float4(kk[0], kk[1], kk[2], kk[3]);
+            *reinterpret_cast<float4*>(sk + kBNK * DT) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+          }
         }
       }
     }
+    u += ub - ua;
+    first_seg = false;
   }
+}
+
+// ---------------------------------------------------------------------------
+// 4. Fixup: one workgroup per key tile. Sums the partials of tiles shared by
+// several dkdv workgroups, zero-fills tiles that no query can see, and leaves
+// tiles one workgroup finished alone untouched.
+template <typename T, int DT, bool CAUSAL>
+__global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p) {
+  const int t = blockIdx.x;
+  const int kt = t / p.ngroups, grp = t % p.ngroups;
+  const int b = grp / p.Hkv, kvh = grp % p.Hkv;
+  const int k0 = kt * kBNK;
+  const int nq = dkdv_nq(kt, p.nqt, CAUSAL);
+  const int nkeys = min(kBNK, p.Sk - k0);
+  constexpr int QPR = DT / 4;
+  if (nq == 0) {
+    for (int e = threadIdx.x; e < nkeys * QPR; e += 256) {
+      const int kr = e / QPR, d = (e % QPR) * 4;
+      if (d >= p.D) continue;
+      const u32x2 z = {0u, 0u};
+      *reinterpret_cast<u32x2*>(p.dk + b * p.dk_sb + kvh * p.dk_sh + (k0 + kr) * p.dk_ss + d) = z;
+      *reinterpret_cast<u32x2*>(p.dv + b * p.dv_sb + kvh * p.dv_sh + (k0 + kr) * p.dv_ss + d) = z;
+    }
+    return;
+  }
+  int64_t base = 0;
+  for (int k = 0; k < kt; ++k) base += (int64_t)p.ngroups * p.G * dkdv_nq(k, p.nqt, CAUSAL);
+  const int64_t first = base + (int64_t)grp * p.G * nq;
+  const int64_t last = first + (int64_t)p.G * nq - 1;
+  const int64_t N = p.nwg;
+  const int64_t w0 = dkdv_owner(first, p.units, N), w1 = dkdv_owner(last, p.units, N);
+  if (w0 == w1) return;
+  for (int e = threadIdx.x; e < nkeys * QPR; e += 256) {
+    const int kr = e / QPR, d = (e % QPR) * 4;
+    if (d >= p.D) continue;
+    float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
+    for (int64_t w = w0; w <= w1; ++w) {
+      const int64_t wu0 = dkdv_u0(w, p.units, N);
+      if (dkdv_u0(w + 1, p.units, N) == wu0) continue;  // empty share: wrote nothing
+      const int side = wu0 >= first ? 0 : 1;
+      const float* slot = p.part + (2 * w + side) * 2 * kBNK * DT + (int64_t)kr * DT + d;
+      const float4 a = *reinterpret_cast<const float4*>(slot);
+      const float4 c = *reinterpret_cast<const float4*>(slot + kBNK * DT);
+      sk.x += a.x; sk.y += a.y; sk.z += a.z; sk.w += a.w;
+      sv.x += c.x; sv.y += c.y; sv.z += c.z; sv.w += c.w;
+    }
+    u32x2 w2;
+    w2[0] = pack2<T>(sk.x, sk.y);
+    w2[1] = pack2<T>(sk.z, sk.w);
+    *reinterpret_cast<u32x2*>(p.dk + b * p.dk_sb + kvh * p.dk_sh + (k0 + kr) * p.dk_ss + d) = w2;
+    w2[0] = pack2<T>(sv.x, sv.y);
+    w2[1] = pack2<T>(sv.z, sv.w);
+    *reinterpret_cast<u32x2*>(p.dv + b * p.dv_sb + kvh * p.dv_sh + (k0 + kr) * p.dv_ss + d) = w2;
+  }
+}
+
+// Stream-K bookkeeping from the host: total units and the workgroup count.
+static int64_t dkdv_total_units(int ngroups, int G, int nqt, int nkt, bool causal) {
+  int64_t U = 0;
+  for (int kt = 0; kt < nkt; ++kt) U += (int64_t)ngroups * G * dkdv_nq(kt, nqt, causal);
+  return U;
+}
+
+static int device_cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    return 256;
+  return n;
+}
+
+static size_t delta_bytes(int64_t B, int64_t Hq, int64_t Sq) {
+  return ((size_t)B * Hq * Sq * sizeof(float) + 255) / 256 * 256;
+}
+
+static size_t partial_bytes(int nwg, int64_t D) {
+  return (size_t)2 * nwg * 2 * kBNK * head_tile(D) * sizeof(float);
 }
 
 template <typename T, int DT>
@@ -468,14 +608,21 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
     if (rc) return rc;
   }
   if (stages & KF_BWD_DKDV) {
-    p.nqt = cdiv(p.Sq, 64);
-    p.nkt = cdiv(p.Sk, 128);
-    const int64_t gk = (int64_t)p.nkt * p.B * p.Hkv;
+    p.nqt = cdiv(p.Sq, kBMQ);
+    p.nkt = cdiv(p.Sk, kBNK);
+    p.units = dkdv_total_units(p.ngroups, p.G, p.nqt, p.nkt, causal);
     if (causal)
-      hipLaunchKernelGGL((dkdv_kernel<T, DT, true>), dim3((unsigned)gk), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((dkdv_kernel<T, DT, true>), dim3((unsigned)p.nwg), dim3(512), 0, stream, p);
     else
-      hipLaunchKernelGGL((dkdv_kernel<T, DT, false>), dim3((unsigned)gk), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((dkdv_kernel<T, DT, false>), dim3((unsigned)p.nwg), dim3(512), 0, stream, p);
     int rc = check_launch("kf_attn_bwd(dkdv)");
+    if (rc) return rc;
+    const int64_t tiles = (int64_t)p.nkt * p.ngroups;
+    if (causal)
+      hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, true>), dim3((unsigned)tiles), dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, false>), dim3((unsigned)tiles), dim3(256), 0, stream, p);
+    rc = check_launch("kf_attn_bwd(dkdv fixup)");
     if (rc) return rc;
   }
   return KF_OK;
@@ -497,9 +644,9 @@ using namespace kf;
 
 extern "C" size_t kf_attn_bwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
                                               int64_t Sk, int64_t D, int causal) {
-  (void)Hkv; (void)Sk; (void)D; (void)causal;
-  const size_t rows = (size_t)(B > 0 ? B : 0) * (size_t)(Hq > 0 ? Hq : 0) * (size_t)(Sq > 0 ? Sq : 0);
-  return ((rows * sizeof(float) + 255) / 256) * 256;
+  (void)Hkv; (void)Sk; (void)causal;
+  if (B <= 0 || Hq <= 0 || Sq <= 0 || D <= 0) return 0;
+  return delta_bytes(B, Hq, Sq) + partial_bytes(device_cu_count(), D);
 }
 
 extern "C" int kf_attn_bwd_stages(int stages, const void* q, const void* k, const void* v,
@@ -525,6 +672,9 @@ extern "C" int kf_attn_bwd_stages(int stages, const void* q, const void* k, cons
     return rc;
   if (lse == nullptr) return set_error(KF_EINVAL, "%s: lse is null", what);
   if (!(scale == scale) || scale - scale != 0.f) return set_error(KF_EINVAL, "%s: scale must be finite", what);
+  if ((rc = check_extent(what, "q", Sq, q_strides[2], D)) || (rc = check_extent(what, "k", Sk, k_strides[2], D)) ||
+      (rc = check_extent(what, "v", Sk, v_strides[2], D)) || (rc = check_extent(what, "dout", Sq, do_strides[2], D)))
+    return rc;
   const size_t need = kf_attn_bwd_workspace_bytes(B, Hq, Hkv, Sq, Sk, D, causal);
   if (workspace == nullptr || workspace_bytes < need)
     return set_error(KF_EINVAL, "%s: workspace of %zu bytes required, got %zu", what, need,
@@ -533,6 +683,8 @@ extern "C" int kf_attn_bwd_stages(int stages, const void* q, const void* k, cons
   p.q = (const uint16_t*)q; p.k = (const uint16_t*)k; p.v = (const uint16_t*)v;
   p.o = (const uint16_t*)o; p.dout = (const uint16_t*)dout; p.lse = lse;
   p.delta = (float*)workspace;
+  p.nwg = device_cu_count();
+  p.part = (float*)((char*)workspace + delta_bytes(B, Hq, Sq));
   p.dq = (uint16_t*)dq; p.dk = (uint16_t*)dk; p.dv = (uint16_t*)dv;
   p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
   p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];
@@ -543,6 +695,8 @@ extern "C" int kf_attn_bwd_stages(int stages, const void* q, const void* k, cons
   p.dk_sb = dk_strides[0]; p.dk_sh = dk_strides[1]; p.dk_ss = dk_strides[2];
   p.dv_sb = dv_strides[0]; p.dv_sh = dv_strides[1]; p.dv_ss = dv_strides[2];
   p.B = (int)B; p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.Sq = (int)Sq; p.Sk = (int)Sk; p.D = (int)D;
+  p.G = (int)(Hq / Hkv);
+  p.ngroups = (int)(B * Hkv);
   p.scale = scale;
   p.scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
