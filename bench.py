@@ -14,14 +14,17 @@ One JSON line on stdout (everything else goes to stderr):
   S = Q K^T, dP = dO V^T, dV, dK = 2x the forward FLOP = 2.7494e11) over its
   average launch time, from HIP events recorded around it on its launch
   stream during the timed steps; peak = MI355X dense fp16 MFMA 2.5 PFLOP/s.
-* ``kernels``: the same live figures for every launch of the step.
+  ``traffic`` is the HBM bytes per dK/dV launch read from rocprofv3
+  FETCH_SIZE + WRITE_SIZE counters (profiles/), calibrated on a copy kernel.
+* ``kernels``: every launch of the step timed on its own, 20 back-to-back
+  launches between two events, after the timed steps.
 * ``decode``: BASELINE config 2 at Sk=16384 (B=2, Hq=8, Hkv=2, Sq=1, D=64,
   fp16): microseconds per call (split-KV kernel + LSE merge) from HIP-graph
   replays of back-to-back calls over 32 rotating K/V sets (537 MB, larger than
   the 256 MB Infinity Cache), and HBM GB/s of the 16,781,376 algorithmic bytes.
 * ``cpu_baseline``: the reference's SDPA path (native-GQA
   scaled_dot_product_attention, fp32, autograd backward) on the host CPU at the
-  full config 3 shape, median of 3 timed steps after one warm-up.
+  full config 3 shape, median of 5 timed steps after one warm-up.
 
 ``--gpus N`` with N > 1 exits with status 2: this build runs on one GPU.
 """
@@ -40,6 +43,11 @@ CFG3 = dict(B=2, Hq=16, Hkv=4, S=4096, D=128)
 CFG2 = dict(B=2, Hq=8, Hkv=2, Sq=1, Sk=16384, D=64)
 PEAK_MFMA_F16 = 2.5e15
 PEAK_HBM = 8.0e12
+# HBM-side bytes per dK/dV launch at config 3 fp16: rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE of the dK/dV dispatch of `bench.py --pmc-sample`, each scaled by the
+# factor the same counter reads for a 512 MiB copy / fill in that program
+# (profiles/dkdv_cfg3_hbm_traffic.md). Re-measure when the dK/dV kernel changes.
+DKDV_TRAFFIC_BYTES = 1.1380e9
 
 
 def log(*a):
@@ -68,24 +76,34 @@ def bench_train(torch, _hip, dtype, steps, warmup):
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     ws = torch.empty(_hip.bwd_workspace_bytes(b, hq, hkv, s, s, d, True), device=q.device,
                      dtype=torch.uint8)
-    names = ("attn_fwd", "bwd_delta", "bwd_dq", "bwd_dkdv")
+
+    def fwd():
+        _hip.fwd(q, k, v, out, lse, causal=True, scale=scale)
+
+    def bwd(stages):
+        _hip.bwd(q, k, v, out, lse, do, dq, dk, dv, causal=True, scale=scale,
+                 workspace=ws, stages=stages)
 
     def step(ev=None):
+        fwd()
+        bwd(_hip.KF_BWD_DELTA | _hip.KF_BWD_DQ)
         if ev is not None:
             ev[0].record()
-        _hip.fwd(q, k, v, out, lse, causal=True, scale=scale)
+        bwd(_hip.KF_BWD_DKDV)
         if ev is not None:
             ev[1].record()
-        for i, st in enumerate((_hip.KF_BWD_DELTA, _hip.KF_BWD_DQ, _hip.KF_BWD_DKDV)):
-            _hip.bwd(q, k, v, out, lse, do, dq, dk, dv, causal=True, scale=scale,
-                     workspace=ws, stages=st)
-            if ev is not None:
-                ev[2 + i].record()
+        bwd(_hip.KF_BWD_DKDV_FIXUP)
 
+    # The launches go to torch's current stream, so events recorded on it
+    # bracket exactly the dK/dV kernel inside the timed steps. torch creates
+    # the HIP event on its first record; recording every event once here keeps
+    # that creation out of the timed region.
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for e in [start, stop] + [x for pair in evs for x in pair]:
+        e.record()
     for _ in range(warmup):
         step()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record()
@@ -95,10 +113,64 @@ def bench_train(torch, _hip, dtype, steps, warmup):
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     ms = start.elapsed_time(stop) / steps
-    per = {n: statistics.mean(e[j].elapsed_time(e[j + 1]) for e in evs) for j, n in enumerate(names)}
+    dkdv_live = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+
+    # Per-kernel figures: each launch repeated back to back between two events
+    # (no event between launches), after the timed steps.
+    def isolated(fn, n=20):
+        fn()
+        torch.cuda.synchronize()
+        a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        z.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(z) / n
+
+    per = {
+        "attn_fwd": isolated(fwd),
+        "bwd_delta": isolated(lambda: bwd(_hip.KF_BWD_DELTA)),
+        "bwd_dq": isolated(lambda: bwd(_hip.KF_BWD_DQ)),
+        "bwd_dkdv": isolated(lambda: bwd(_hip.KF_BWD_DKDV)),
+        "bwd_dkdv_fixup": isolated(lambda: bwd(_hip.KF_BWD_DKDV_FIXUP)),
+    }
     f = fwd_flops(b, hq, s, d)
-    work = {"attn_fwd": f, "bwd_delta": 0.0, "bwd_dq": 0.5 * f, "bwd_dkdv": 2.0 * f}
-    return ms, wall_ms, per, work, 3.5 * f
+    work = {"attn_fwd": f, "bwd_delta": 0.0, "bwd_dq": 0.5 * f, "bwd_dkdv": 2.0 * f,
+            "bwd_dkdv_fixup": 0.0}
+    return ms, wall_ms, dkdv_live, per, work, 3.5 * f
+
+
+def pmc_sample(torch, _hip, dtype):
+    """One config 3 step (forward, delta, dQ, dK/dV, fixup) followed by a
+    512 MiB fill and a 512 MiB device copy, for per-dispatch counter runs
+    (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE): the fill and copy have known
+    HBM traffic (0 + 512 MiB and 512 + 512 MiB) and calibrate the counters'
+    scale for the dK/dV dispatch."""
+    c = CFG3
+    b, hq, hkv, s, d = c["B"], c["Hq"], c["Hkv"], c["S"], c["D"]
+    scale = 1.0 / math.sqrt(d)
+    q = seeded(torch, (b, hq, s, d), 301, dtype, 0.5)
+    k = seeded(torch, (b, hkv, s, d), 302, dtype, 0.5)
+    v = seeded(torch, (b, hkv, s, d), 303, dtype, 0.5)
+    do = seeded(torch, (b, hq, s, d), 304, dtype)
+    out = torch.empty_like(q)
+    lse = torch.empty((b, hq, s), device=q.device, dtype=torch.float32)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = torch.empty(_hip.bwd_workspace_bytes(b, hq, hkv, s, s, d, True), device=q.device,
+                     dtype=torch.uint8)
+    _hip.fwd(q, k, v, out, lse, causal=True, scale=scale)
+    for st in (_hip.KF_BWD_DELTA, _hip.KF_BWD_DQ, _hip.KF_BWD_DKDV, _hip.KF_BWD_DKDV_FIXUP):
+        _hip.bwd(q, k, v, out, lse, do, dq, dk, dv, causal=True, scale=scale, workspace=ws,
+                 stages=st)
+    n = 256 << 20
+    src = torch.empty(n, device=q.device, dtype=torch.float16)
+    dst = torch.empty_like(src)
+    src.fill_(1.0)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"dispatches": ["attn_fwd", "bwd_delta", "bwd_dq", "bwd_dkdv", "bwd_dkdv_fixup",
+                           "fill 512 MiB", "copy 512 MiB"], "copy_bytes": 2 * n}
 
 
 def bench_api(torch, kf, dtype, steps, warmup):
@@ -194,7 +266,7 @@ def cpu_baseline(dtype_name):
 
     step()
     times = []
-    for _ in range(3):
+    for _ in range(5):
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)
@@ -211,18 +283,22 @@ def cpu_baseline(dtype_name):
     return {"value": work / t / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "sample": (f"full config 3 shape (B=2 Hq=16 Hkv=4 S=4096 D=128 causal), fp32 "
                        f"torch SDPA fwd + autograd bwd as the reference's _sdpa path "
-                       f"(oracle.sdpa_cpu), median of 3 steps = {t:.3f} s on {cores} "
+                       f"(oracle.sdpa_cpu), median of 5 steps = {t:.3f} s on {cores} "
                        f"threads of {model or 'the host CPU'}")}
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n", 1)[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100,
+                    help="untimed steps first; ~0.1 s of work lets the GPU clocks settle")
     ap.add_argument("--dtype", choices=("float16", "bfloat16"), default="float16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--pmc-sample", action="store_true",
+                    help="run one config 3 step plus a calibration fill/copy for rocprofv3 "
+                         "--pmc and exit (prints no bench line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -244,9 +320,14 @@ def main() -> int:
     dtype = getattr(torch, args.dtype)
     _hip.lib()
     log(f"device: {torch.cuda.get_device_properties(0).gcnArchName}")
+    if args.pmc_sample:
+        log(json.dumps(pmc_sample(torch, _hip, dtype)))
+        return 0
 
-    ms, wall_ms, per, work, step_flops = bench_train(torch, _hip, dtype, args.steps, args.warmup)
-    log(f"train step: {ms:.4f} ms (GPU events), {wall_ms:.4f} ms (wall); per kernel {per}")
+    ms, wall_ms, dkdv_live, per, work, step_flops = bench_train(torch, _hip, dtype, args.steps,
+                                                                args.warmup)
+    log(f"train step: {ms:.4f} ms (GPU events), {wall_ms:.4f} ms (wall); dkdv live "
+        f"{dkdv_live:.4f} ms; isolated per kernel {per}")
     api_ms = bench_api(torch, kf, dtype, max(5, args.steps // 5), 2)
     log(f"public API step: {api_ms:.4f} ms")
     kernels = {}
@@ -254,12 +335,13 @@ def main() -> int:
         kernels[n] = {"ms": t, "tflops": work[n] / (t * 1e-3) / 1e12 if work[n] else None,
                       "frac": work[n] / (t * 1e-3) / PEAK_MFMA_F16 if work[n] else None}
     dom = "bwd_dkdv"
-    dom_t = per[dom] * 1e-3
+    dom_t = dkdv_live * 1e-3
     roofline = {"kernel": "dkdv_kernel (dK/dV, key-stationary backward)", "bound": "mfma",
                 "achieved": work[dom] / dom_t / 1e12, "peak": PEAK_MFMA_F16 / 1e12,
-                "unit": "TFLOP/s", "frac": work[dom] / dom_t / PEAK_MFMA_F16, "traffic": None,
-                "work_per_launch": work[dom],
-                "avg_launch_ms": per[dom]}
+                "unit": "TFLOP/s", "frac": work[dom] / dom_t / PEAK_MFMA_F16,
+                "traffic": DKDV_TRAFFIC_BYTES, "work_per_launch": work[dom],
+                "avg_launch_ms": dkdv_live,
+                "timing": "HIP events around each dK/dV launch on its stream in the timed steps"}
     decode = None if args.no_decode else bench_decode(torch, _hip, torch.float16, CFG2["Sk"])
     if decode:
         log(f"decode: {decode}")

@@ -82,14 +82,22 @@ int kf_attn_bwd(const void* q, const void* k, const void* v, const void* o, cons
                 size_t workspace_bytes, void* stream);
 
 /*
- * The three launches of kf_attn_bwd, selectable by a mask of KF_BWD_* bits and
- * run in the order delta, dq, dkdv (the delta stage writes the fp32 row deltas
- * into the workspace; dq and dkdv read them). kf_attn_bwd is this call with all
- * three bits. Same launch split as the reference backward, whose dQ and dK/dV
- * kernels are separate launches (triton_backward.py:374-419); used to time
- * each kernel on its own.
+ * The launches of kf_attn_bwd, selectable by a mask of KF_BWD_* bits and run
+ * in the order delta, dq, dkdv, dkdv fixup: the delta stage writes the fp32 row
+ * deltas into the workspace (dq and dkdv read them); dkdv writes dK/dV of
+ * tiles it finishes alone and fp32 partials of shared tiles into the
+ * workspace; the fixup completes dK/dV from those partials. kf_attn_bwd is
+ * this call with KF_BWD_ALL. Same launch split as the reference backward,
+ * whose dQ and dK/dV kernels are separate launches
+ * (triton_backward.py:374-419); used to time each kernel on its own.
  */
-enum kf_bwd_stage { KF_BWD_DELTA = 1, KF_BWD_DQ = 2, KF_BWD_DKDV = 4 };
+enum kf_bwd_stage {
+  KF_BWD_DELTA = 1,
+  KF_BWD_DQ = 2,
+  KF_BWD_DKDV = 4,
+  KF_BWD_DKDV_FIXUP = 8,
+  KF_BWD_ALL = 15
+};
 int kf_attn_bwd_stages(int stages, const void* q, const void* k, const void* v, const void* o,
                        const float* lse, const void* dout, void* dq, void* dk, void* dv,
                        int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,

@@ -21,8 +21,8 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "libkotflash_amd.so"
 ABI_VERSION = 1
 KF_F16, KF_BF16 = 0, 1
-KF_BWD_DELTA, KF_BWD_DQ, KF_BWD_DKDV = 1, 2, 4
-KF_BWD_ALL = KF_BWD_DELTA | KF_BWD_DQ | KF_BWD_DKDV
+KF_BWD_DELTA, KF_BWD_DQ, KF_BWD_DKDV, KF_BWD_DKDV_FIXUP = 1, 2, 4, 8
+KF_BWD_ALL = KF_BWD_DELTA | KF_BWD_DQ | KF_BWD_DKDV | KF_BWD_DKDV_FIXUP
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int

@@ -617,12 +617,17 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
       hipLaunchKernelGGL((dkdv_kernel<T, DT, false>), dim3((unsigned)p.nwg), dim3(512), 0, stream, p);
     int rc = check_launch("kf_attn_bwd(dkdv)");
     if (rc) return rc;
+  }
+  if (stages & KF_BWD_DKDV_FIXUP) {
+    p.nqt = cdiv(p.Sq, kBMQ);
+    p.nkt = cdiv(p.Sk, kBNK);
+    p.units = dkdv_total_units(p.ngroups, p.G, p.nqt, p.nkt, causal);
     const int64_t tiles = (int64_t)p.nkt * p.ngroups;
     if (causal)
       hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, true>), dim3((unsigned)tiles), dim3(256), 0, stream, p);
     else
       hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, false>), dim3((unsigned)tiles), dim3(256), 0, stream, p);
-    rc = check_launch("kf_attn_bwd(dkdv fixup)");
+    int rc = check_launch("kf_attn_bwd(dkdv fixup)");
     if (rc) return rc;
   }
   return KF_OK;
@@ -659,7 +664,7 @@ extern "C" int kf_attn_bwd_stages(int stages, const void* q, const void* k, cons
                                   const int64_t* dv_strides, float scale, int causal, int dtype,
                                   void* workspace, size_t workspace_bytes, void* stream) {
   const char* what = "kf_attn_bwd";
-  if (stages <= 0 || stages > (KF_BWD_DELTA | KF_BWD_DQ | KF_BWD_DKDV))
+  if (stages <= 0 || stages > KF_BWD_ALL)
     return set_error(KF_EINVAL, "%s: stages must be a non-empty KF_BWD_* mask", what);
   int rc = check_attn_common(what, B, Hq, Hkv, Sq, Sk, D, dtype);
   if (rc) return rc;
@@ -713,7 +718,7 @@ extern "C" int kf_attn_bwd(const void* q, const void* k, const void* v, const vo
                            const int64_t* dk_strides, const int64_t* dv_strides, float scale,
                            int causal, int dtype, void* workspace, size_t workspace_bytes,
                            void* stream) {
-  return kf_attn_bwd_stages(KF_BWD_DELTA | KF_BWD_DQ | KF_BWD_DKDV, q, k, v, o, lse, dout, dq, dk,
+  return kf_attn_bwd_stages(KF_BWD_ALL, q, k, v, o, lse, dout, dq, dk,
                             dv, B, Hq, Hkv, Sq, Sk, D, q_strides, k_strides, v_strides, o_strides,
                             do_strides, dq_strides, dk_strides, dv_strides, scale, causal, dtype,
                             workspace, workspace_bytes, stream);
