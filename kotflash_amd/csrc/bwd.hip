@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_index();
   const int l32 = lane & 31, h32 = lane >> 5;
 
   // Longest query tiles first; KV groups kept on one XCD as in the forward.
@@ -211,6 +211,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
     gload(0);
     sstore(0);
   }
+  wait_all_memory();
   __syncthreads();
 
   const int wq0 = q0 + wave * 32;
@@ -234,15 +235,18 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
         dp = Elem<T>::mfma(a2, dof[ks], dp);
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        bool valid = true;
-        if (need_mask) {
-          const int key = kb0 + 8 * (r >> 2) + 4 * h32 + (r & 3);
-          valid = key < p.Sk && (!CAUSAL || key <= qrow);
+      for (int r = 0; r < 16; ++r) s[r] = fmaf(s[r], p.scale_log2, -lse2);
+      if (need_mask) {
+        // Key kb0 + c is visible iff c < lim.
+        const int lim = CAUSAL ? min(p.Sk - kb0, qrow - kb0 + 1) : p.Sk - kb0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int c = 8 * (r >> 2) + 4 * h32 + (r & 3);
+          s[r] = c < lim ? s[r] : kNegInf;
         }
-        const float pv = valid ? fast_exp2(s[r] * p.scale_log2 - lse2) : 0.f;
-        dp[r] = pv * (dp[r] - dlt);
       }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dp[r] = fast_exp2(s[r]) * (dp[r] - dlt);
       const u32x4 ds0 = pack8<T>(dp, 0), ds1 = pack8<T>(dp, 8);
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
@@ -298,7 +302,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(const BwdParams p) {
   uint16_t* const Qstage = smem + 2 * KVT;  // [buf][Q | dO]
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_index();
   const int l32 = lane & 31, h32 = lane >> 5;
   const int kbw = wave & 3, qh = wave >> 2;
 
@@ -429,12 +433,12 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(const BwdParams p) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int r = 4 * g4 + e;
-            bool valid = true;
+            float x = fmaf(s[r], p.scale_log2, -l4[e]);
             if (need_mask) {
               const int qi = qw0 + 8 * g4 + 4 * h32 + e;
-              valid = qi < p.Sq && key_ok && (!CAUSAL || key <= qi);
+              x = (qi < p.Sq && key_ok && (!CAUSAL || key <= qi)) ? x : kNegInf;
             }
-            const float pv = valid ? fast_exp2(s[r] * p.scale_log2 - l4[e]) : 0.f;
+            const float pv = fast_exp2(x);
             s[r] = pv;
             dp[r] = pv * (dp[r] - d4[e]);
           }

@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM_ELEMS];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_index();
   const int l32 = lane & 31, h32 = lane >> 5;
 
   int bid = blockIdx.x;
@@ -137,6 +137,7 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db) oacc[qb][db] = zero16();
   }
+  wait_all_memory();
 
   for (int st = 0; st < nst; ++st) {
     {

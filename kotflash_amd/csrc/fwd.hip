@@ -22,7 +22,10 @@
 // (:69-76), P rounded to the input dtype before the PV product (:131,:135),
 // O stored in the input dtype (:139-158), LSE = m + ln(l) in fp32 (:160-165).
 // exp/log use the hardware base-2 instructions with the scale folded into
-// log2(e).
+// log2(e). One deliberate difference: the denominator l accumulates the
+// rounded P that the PV product consumes (fp32 dot2 sums of the packed
+// values), where the reference sums P before rounding (:128); the two differ
+// by far less than the rounding of O itself.
 #include "kf_common.hpp"
 #include "kf_host.hpp"
 
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = wave_index();
   const int l32 = lane & 31, h32 = lane >> 5;
 
   int qt, b, h;
@@ -109,6 +112,16 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
       const uint32_t off = (row < p.Sq && d < p.D) ? (uint32_t)(row * p.q_ss + d) * 2u : kOOB;
       qf[qb][ks] = buf_load16(qr, off);
     }
+  }
+  // Scores are reduced (row max) before scaling, which needs a positive scale:
+  // for a negative one, Q is negated (an exact sign flip of every element) and
+  // |scale| used, giving the same scaled scores.
+  const float sl2 = fabsf(p.scale_log2);
+  if (p.scale_log2 < 0.f) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) qf[qb][ks] ^= 0x80008000u;
   }
 
   f32x16 oacc[QB][NDB];
@@ -165,6 +178,7 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
     gload(0);
     sstore(0);
   }
+  wait_all_memory();
   __syncthreads();
 
   for (int it = 0; it < ntiles; ++it) {
@@ -197,22 +211,27 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
       u32x4 pk[QB][4];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
-        const int qrow = wq0 + qb * 32 + l32;
+        if (need_mask) {
+          // Key kbase + c is visible iff c < lim (c < Sk - kbase, and c <= row
+          // - kbase when causal).
+          const int qrow = wq0 + qb * 32 + l32;
+          const int lim = CAUSAL ? min(p.Sk - kbase, qrow - kbase + 1) : p.Sk - kbase;
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int c = 32 * kb + 8 * (r >> 2) + 4 * h32 + (r & 3);
+              s[qb][kb][r] = c < lim ? s[qb][kb][r] : kNegInf;
+            }
+          }
+        }
         float mx = kNegInf;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float x = s[qb][kb][r] * p.scale_log2;
-            if (need_mask) {
-              const int key = kbase + 32 * kb + 8 * (r >> 2) + 4 * h32 + (r & 3);
-              x = (key >= p.Sk || (CAUSAL && key > qrow)) ? kNegInf : x;
-            }
-            s[qb][kb][r] = x;
-            mx = fmaxf(mx, x);
-          }
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][kb][r]);
         }
-        mx = wave_xor32_max(mx);
+        mx = wave_xor32_max(mx) * sl2;
         // Lazy rescale: move the reference max only when a score exceeds it
         // by more than kRescaleThreshold (O and l are still zero while the
         // max is -inf, so the first finite max is adopted without rescaling).
@@ -229,19 +248,23 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
           }
         }
         const float msub = (m_i[qb] == kNegInf) ? 0.f : m_i[qb];
-        float rs = 0.f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float e = fast_exp2(s[qb][kb][r] - msub);
-            s[qb][kb][r] = e;
-            rs += e;
-          }
+          for (int r = 0; r < 16; ++r) s[qb][kb][r] = fast_exp2(fmaf(s[qb][kb][r], sl2, -msub));
         }
-        l_i[qb] += rs;
 #pragma unroll
         for (int st = 0; st < 4; ++st) pk[qb][st] = pack8<T>(s[qb][st >> 1], 8 * (st & 1));
+        // The denominator sums the rounded P that the PV product consumes.
+        float rs0 = 0.f, rs1 = 0.f;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          rs0 = sum2_acc<T>(pk[qb][st][0], rs0);
+          rs1 = sum2_acc<T>(pk[qb][st][1], rs1);
+          rs0 = sum2_acc<T>(pk[qb][st][2], rs0);
+          rs1 = sum2_acc<T>(pk[qb][st][3], rs1);
+        }
+        l_i[qb] += rs0 + rs1;
       }
 
 #pragma unroll
@@ -304,12 +327,11 @@ template <typename T>
 static int dispatch_fwd(const FwdParams& p, bool causal, hipStream_t stream) {
   // One 32-row block per wave at two waves per SIMD: while one wave runs its
   // softmax on the VALU the other keeps the MFMA pipe busy.
-  const bool qb2 = false;
   switch (head_tile(p.D)) {
-    case 32: return qb2 ? launch_fwd<T, 32, 2>(p, causal, stream) : launch_fwd<T, 32, 1>(p, causal, stream);
-    case 64: return qb2 ? launch_fwd<T, 64, 2>(p, causal, stream) : launch_fwd<T, 64, 1>(p, causal, stream);
-    case 96: return qb2 ? launch_fwd<T, 96, 2>(p, causal, stream) : launch_fwd<T, 96, 1>(p, causal, stream);
-    default: return qb2 ? launch_fwd<T, 128, 2>(p, causal, stream) : launch_fwd<T, 128, 1>(p, causal, stream);
+    case 32: return launch_fwd<T, 32, 1>(p, causal, stream);
+    case 64: return launch_fwd<T, 64, 1>(p, causal, stream);
+    case 96: return launch_fwd<T, 96, 1>(p, causal, stream);
+    default: return launch_fwd<T, 128, 1>(p, causal, stream);
   }
 }
 

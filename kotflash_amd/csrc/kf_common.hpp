@@ -69,9 +69,14 @@ template <> struct Elem<__bf16> {
   }
 };
 
+// Two floats -> two packed 16-bit elements, round to nearest even, in one
+// v_cvt_pk_{f16,bf16}_f32.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 template <typename T>
 __device__ inline uint32_t pack2(float lo, float hi) {
-  return (uint32_t)Elem<T>::bits(lo) | ((uint32_t)Elem<T>::bits(hi) << 16);
+  typedef T t2 __attribute__((ext_vector_type(2)));
+  const f32x2 x = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, t2));
 }
 
 // Eight consecutive accumulator registers -> one 8-element MFMA operand.
@@ -161,8 +166,43 @@ __device__ inline u32x4 lds_read_tr_operand(const uint16_t* tile, int stride, in
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
-__device__ inline float wave_xor32_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
-__device__ inline float wave_xor32_sum(float x) { return x + __shfl_xor(x, 32); }
+// Combine the two 32-lane halves of a wave. v_permlane32_swap (gfx950, VALU)
+// exchanges the upper half of its first operand with the lower half of its
+// second; with both operands x the two results hold (x_lo, x_lo) and
+// (x_hi, x_hi), so max/sum of the pair is the cross-half reduction in every
+// lane, bit-identical in both halves.
+__device__ inline float wave_xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float wave_xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Wave index inside the workgroup as a wave-uniform (scalar) value, so that
+// conditions built from it compile to scalar branches.
+__device__ inline int wave_index() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+// Wait for every outstanding memory operation of the wave. Placed after
+// prologue loads whose completion the compiler cannot otherwise prove on all
+// paths into a loop; without it, the loop waits on them (and on every load
+// issued after them) at its first use of those registers in each iteration.
+__device__ inline void wait_all_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+// acc + x.lo + x.hi for two packed 16-bit elements, accumulated in fp32
+// (v_dot2c_f32_f16 / _bf16 against (1, 1)).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+template <typename T> __device__ inline float sum2_acc(uint32_t x, float acc);
+template <> __device__ inline float sum2_acc<_Float16>(uint32_t x, float acc) {
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x), one, acc, false);
+}
+template <> __device__ inline float sum2_acc<__bf16>(uint32_t x, float acc) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x), one, acc, false);
+}
 
 __host__ __device__ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
