@@ -7,15 +7,13 @@
 //      SIMD): per key tile it recomputes S^T = K Q^T and dP^T = V dO^T, forms
 //      dS^T = P^T (dP^T - delta) with P = exp(scale S - LSE), and accumulates
 //      dQ^T += K^T dS^T; dQ = scale * dQ (reference :17-91).
-//   3. dkdv_kernel (key-stationary, 8 waves per workgroup): a key tile is 128
-//      keys of one (batch, kv_head) held in LDS; for every query head of the
-//      GQA group and every 64-row query tile the kernel recomputes S = Q K^T
-//      and dP = dO V^T and accumulates dV^T += dO^T P and dK^T += Q^T dS in
-//      registers (wave w owns keys 32 (w % 4) .. +31 and query rows
-//      32 (w / 4) .. +31 of each tile; the two query halves are summed in LDS
-//      when the tile is done). The group sum over query heads therefore happens
-//      in registers (reference :94-195, group loop :136-137, products
-//      :183-184). Work is split stream-K style: the (key tile, head, query tile)
+//   3. dkdv_kernel (key-stationary, 4 waves, one per SIMD): a key tile is 128
+//      keys of one (batch, kv_head); wave w keeps keys 32 w .. +31 in
+//      registers. For every query head of the GQA group and every 64-row query
+//      tile the kernel recomputes S = Q K^T and dP = dO V^T and accumulates
+//      dV^T += dO^T P and dK^T += Q^T dS in registers, so the group sum over
+//      query heads happens in registers (reference :94-195, group loop
+//      :136-137, products :183-184). Work is split stream-K style: the (key tile, head, query tile)
 //      units of all tiles are laid end to end and every workgroup takes an
 //      equal share, so causal tiles of very different sizes still keep every
 //      CU busy until the end. A tile shared by several workgroups is written
@@ -280,31 +278,31 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
 
 // ---------------------------------------------------------------------------
 // 3. dK/dV, key-stationary, stream-K over (key tile, head, query tile) units.
+// Four waves, one per SIMD (the 512-register budget lets the dK/dV
+// accumulators live in accumulation registers). Wave w owns keys
+// 32 w .. 32 w + 31 of the 128-key tile and keeps their K and V rows in
+// registers as MFMA B operands for the whole tile; per unit it covers all 64
+// query rows, which the workgroup stages (Q, dO, LSE, delta) through LDS,
+// double-buffered. Per unit and 32-row query block:
+//   S  = Q K^T,  dP = dO V^T            (A = Q / dO rows from LDS, B = K / V)
+//   P  = exp2(scale log2e S - LSE log2e),  dS = P (dP - delta)
+//   dV^T += dO^T P,  dK^T += Q^T dS      (A = transposed LDS reads, B = P / dS
+//                                         straight from the S / dP registers)
 template <typename T, int DT, bool CAUSAL>
-__global__ __launch_bounds__(512, 1) void dkdv_kernel(const BwdParams p) {
-  constexpr int KSTR = DT + 8;   // K/V tiles: b128 reads
+__global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
   constexpr int QSTR = DT + 16;  // Q/dO tiles: b128 and transposed reads
-  constexpr int KVT = kBNK * KSTR;
   constexpr int QT = kBMQ * QSTR;
   constexpr int CPR = DT / 8;
-  constexpr int QCH = kBMQ * CPR;          // 16-byte chunks of a Q (or dO) tile
-  constexpr int QCPT = (QCH + 511) / 512;  // per thread
-  constexpr int KVCPT = kBNK * CPR / 512;  // K (or V) tile chunks per thread
+  constexpr int QCPT = kBMQ * CPR / 256;  // 16-byte chunks per thread of a Q (or dO) tile
   constexpr int NKS = DT / 16;
   constexpr int NDB = DT / 32;
-  constexpr int RSTR = DT + 1;             // padded rows of the flush reduction
-  static_assert(kBNK * RSTR * 4 <= 2 * QT * 2 * 2, "flush reduction must fit the Q/dO stages");
-  static_assert(kBNK * RSTR * 4 <= 2 * KVT * 2, "flush reduction must fit the K/V tiles");
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * KVT + 4 * QT];
-  __shared__ __attribute__((aligned(16))) float rowstat[2][2][kBMQ];  // [buf][lse2, delta][row]
-  uint16_t* const Ks = smem;
-  uint16_t* const Vs = smem + KVT;
-  uint16_t* const Qstage = smem + 2 * KVT;  // [buf][Q | dO]
+  static_assert(kBMQ * CPR % 256 == 0, "Q tile chunks must divide over the workgroup");
+  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * QT];        // [buf][Q | dO]
+  __shared__ __attribute__((aligned(16))) float rowstat[2][2][kBMQ];   // [buf][lse2, delta][row]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
   const int l32 = lane & 31, h32 = lane >> 5;
-  const int kbw = wave & 3, qh = wave >> 2;
 
   const int64_t N = gridDim.x;
   int64_t u = dkdv_u0(blockIdx.x, p.units, N);
@@ -334,21 +332,21 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(const BwdParams p) {
     const int ub = (int)min((int64_t)per_tile, ua + (uend - u));
     const int b = grp / p.Hkv, kvh = grp % p.Hkv;
     const int k0 = kt * kBNK;
+    const int kw0 = k0 + wave * 32;  // first key of this wave
+    const int key = kw0 + l32;
+    const bool key_ok = key < p.Sk;
 
-    __syncthreads();  // previous segment's flush has finished with LDS
+    // This wave's K and V rows as B operands: lane = key, slots = head_dim.
+    u32x4 kf[NKS], vf[NKS];
     {
       const auto kr = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, rows_extent(p.Sk, p.k_ss, p.D));
       const auto vr = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, rows_extent(p.Sk, p.v_ss, p.D));
 #pragma unroll
-      for (int c = 0; c < KVCPT; ++c) {
-        const int e = tid + 512 * c;
-        const int row = e / CPR, col = e % CPR;
-        const int key = k0 + row;
-        const bool ok = key < p.Sk && col * 8 < p.D;
-        const u32x4 kk = buf_load16(kr, ok ? (uint32_t)(key * p.k_ss + col * 8) * 2u : kOOB);
-        const u32x4 vv = buf_load16(vr, ok ? (uint32_t)(key * p.v_ss + col * 8) * 2u : kOOB);
-        lds_write16(Ks + row * KSTR + col * 8, kk);
-        lds_write16(Vs + row * KSTR + col * 8, vv);
+      for (int ks = 0; ks < NKS; ++ks) {
+        const int d = 16 * ks + 8 * h32;
+        const bool ok = key_ok && d < p.D;
+        kf[ks] = buf_load16(kr, ok ? (uint32_t)(key * p.k_ss + d) * 2u : kOOB);
+        vf[ks] = buf_load16(vr, ok ? (uint32_t)(key * p.v_ss + d) * 2u : kOOB);
       }
     }
 #pragma unroll
@@ -366,148 +364,200 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(const BwdParams p) {
       const auto dor = make_rsrc(p.dout + b * p.do_sb + h * p.do_sh, rows_extent(p.Sq, p.do_ss, p.D));
 #pragma unroll
       for (int c = 0; c < QCPT; ++c) {
-        const int e = tid + 512 * c;
+        const int e = tid + 256 * c;
         const int row = e / CPR, col = e % CPR;
         const int qi = qbase + row;
-        const bool ok = e < QCH && qi < p.Sq && col * 8 < p.D;
+        const bool ok = qi < p.Sq && col * 8 < p.D;
         qreg[c] = buf_load16(qr, ok ? (uint32_t)(qi * p.q_ss + col * 8) * 2u : kOOB);
         dreg[c] = buf_load16(dor, ok ? (uint32_t)(qi * p.do_ss + col * 8) * 2u : kOOB);
       }
       if (tid < kBMQ) {
         const int qi = qbase + tid;
         const int64_t rl = ((int64_t)b * p.Hq + h) * p.Sq + qi;
-        st_l = qi < p.Sq ? p.lse[rl] * kLog2e : 0.f;
+        // Raw values here; the scaling waits until sstore so that issuing
+        // the loads never waits for them.
+        st_l = qi < p.Sq ? p.lse[rl] : 0.f;
         st_d = qi < p.Sq ? p.delta[rl] : 0.f;
       }
     };
     auto sstore = [&](int buf) {
-      uint16_t* Qs = Qstage + buf * 2 * QT;
+      uint16_t* Qs = smem + buf * 2 * QT;
       uint16_t* Ds = Qs + QT;
 #pragma unroll
       for (int c = 0; c < QCPT; ++c) {
-        const int e = tid + 512 * c;
-        if (e < QCH) {
-          const int row = e / CPR, col = e % CPR;
-          lds_write16(Qs + row * QSTR + col * 8, qreg[c]);
-          lds_write16(Ds + row * QSTR + col * 8, dreg[c]);
-        }
+        const int e = tid + 256 * c;
+        const int row = e / CPR, col = e % CPR;
+        lds_write16(Qs + row * QSTR + col * 8, qreg[c]);
+        lds_write16(Ds + row * QSTR + col * 8, dreg[c]);
       }
       if (tid < kBMQ) {
-        rowstat[buf][0][tid] = st_l;
+        rowstat[buf][0][tid] = st_l * kLog2e;
         rowstat[buf][1][tid] = st_d;
       }
     };
 
-    const int key = k0 + kbw * 32 + l32;
-    const bool key_ok = key < p.Sk;
+    // One unit: both 32-row query blocks (qb) of the staged tile against this
+    // wave's 32 keys. With `diag` the causal mask (key <= row) is applied;
+    // otherwise its comparison is made to pass for every element (one body
+    // for both cases keeps the register footprint of a single copy).
+    //
+    // With one wave per SIMD nothing else hides latency, so the unit is
+    // software-pipelined by hand and the order pinned with scheduling fences:
+    //   phase 1: S/dP MFMAs of qb 0       | LDS operand reads of qb 1
+    //   phase 2: S/dP MFMAs of qb 1       | softmax of qb 0, transposed reads of qb 0
+    //   phase 3: dV/dK MFMAs of qb 0      | softmax of qb 1, transposed reads of qb 1
+    //   phase 4: dV/dK MFMAs of qb 1
+    // The MFMAs run on the matrix core while the interleaved VALU and LDS
+    // instructions of the same wave issue.
+    auto unit = [&](const uint16_t* Qs, const uint16_t* Ds, int buf, int qrow0, bool diag) {
+      constexpr int NSD = 2 * NKS;  // S/dP MFMAs per block
+      constexpr int NVK = 4 * NDB;  // dV/dK MFMAs per block
+      u32x4 aop[2][NSD];            // S/dP A operands: [2 ks] = Q, [2 ks + 1] = dO
+      u32x4 top[2][NVK];            // dV/dK A operands: [4 db + j], j = dO lo/hi, Q lo/hi
+      f32x16 s[2], dp[2];
+      f32x4 l4[2][4], d4[2][4];
+      u32x4 pk[2][4];               // P lo/hi, dS lo/hi
+      int t[2];
+
+      auto read_sd = [&](int qb, int i) {
+        const int ks = i >> 1;
+        const uint16_t* base = (i & 1) ? Ds : Qs;
+        aop[qb][i] = lds_read16(base + (qb * 32 + l32) * QSTR + 16 * ks + 8 * h32);
+      };
+      auto mfma_sd = [&](int qb, int i) {
+        const int ks = i >> 1;
+        if (i & 1)
+          dp[qb] = Elem<T>::mfma(aop[qb][i], vf[ks], dp[qb]);
+        else
+          s[qb] = Elem<T>::mfma(aop[qb][i], kf[ks], s[qb]);
+      };
+      auto read_stats = [&](int qb) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int rl = qb * 32 + 8 * g4 + 4 * h32;
+          l4[qb][g4] = *reinterpret_cast<const f32x4*>(&rowstat[buf][0][rl]);
+          d4[qb][g4] = *reinterpret_cast<const f32x4*>(&rowstat[buf][1][rl]);
+        }
+        // key <= row  <=>  key - (block row 0) - 4 h <= 8 (r/4) + r % 4
+        t[qb] = CAUSAL && diag ? key - (qrow0 + 32 * qb) - 4 * h32 : -(1 << 30);
+      };
+      // S layout: lane = key, register r = query row 8 (r/4) + 4 h + r % 4.
+      auto soft = [&](int qb, int r) {
+        const int g4 = r >> 2, e = r & 3;
+        float x = fmaf(s[qb][r], p.scale_log2, -l4[qb][g4][e]);
+        if (CAUSAL) x = t[qb] <= 8 * g4 + e ? x : kNegInf;
+        const float pv = fast_exp2(x);
+        s[qb][r] = pv;
+        dp[qb][r] = pv * (dp[qb][r] - d4[qb][g4][e]);
+        if (r == 7) {
+          pk[qb][0] = pack8<T>(s[qb], 0);
+          pk[qb][2] = pack8<T>(dp[qb], 0);
+        } else if (r == 15) {
+          pk[qb][1] = pack8<T>(s[qb], 8);
+          pk[qb][3] = pack8<T>(dp[qb], 8);
+        }
+      };
+      auto read_tr = [&](int qb, int j) {
+        const int db = j >> 2, w = j & 3;
+        top[qb][j] = lds_read_tr_operand((w < 2) ? Ds : Qs, QSTR, qb * 32 + 16 * (w & 1), 32 * db, lane);
+      };
+      auto mfma_vk = [&](int qb, int j) {
+        const int db = j >> 2, w = j & 3;
+        if (w < 2)
+          dv[db] = Elem<T>::mfma(top[qb][j], pk[qb][w], dv[db]);
+        else
+          dk[db] = Elem<T>::mfma(top[qb][j], pk[qb][w], dk[db]);
+      };
+
+      s[0] = s[1] = dp[0] = dp[1] = zero16();
+#pragma unroll
+      for (int i = 0; i < NSD; ++i) read_sd(0, i);
+      read_stats(0);
+      read_stats(1);
+      __builtin_amdgcn_sched_barrier(0);
+      // phase 1
+#pragma unroll
+      for (int i = 0; i < NSD; ++i) {
+        mfma_sd(0, i);
+        read_sd(1, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // phase 2
+      constexpr int P2 = NSD > 16 ? NSD : 16;
+#pragma unroll
+      for (int i = 0; i < P2; ++i) {
+        if (i < NSD) mfma_sd(1, i);
+        if (i < 16) soft(0, i);
+        if (i < NVK) read_tr(0, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // phase 3
+      constexpr int P3 = NVK > 16 ? NVK : 16;
+#pragma unroll
+      for (int i = 0; i < P3; ++i) {
+        if (i < NVK) mfma_vk(0, i);
+        if (i < 16) soft(1, i);
+        if (i < NVK) read_tr(1, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // phase 4
+#pragma unroll
+      for (int i = 0; i < NVK; ++i) mfma_vk(1, i);
+    };
+
+    __syncthreads();  // every wave is done with the previous segment's stages
     gload(ua);
     sstore(0);
+    wait_all_memory();
     __syncthreads();
     for (int it = ua; it < ub; ++it) {
       const int buf = (it - ua) & 1;
       if (it + 1 < ub) gload(it + 1);
       const int g = it / nq;
-      const int qt = qs + (it - g * nq);
-      const int qw0 = qt * kBMQ + qh * 32;  // first query row of this wave
-      const uint16_t* Qs = Qstage + buf * 2 * QT;
+      const int qrow0 = (qs + (it - g * nq)) * kBMQ;  // first query row of the unit
+      const uint16_t* Qs = smem + buf * 2 * QT;
       const uint16_t* Ds = Qs + QT;
-      const bool active = !CAUSAL || qw0 + 31 >= k0 + kbw * 32;
-      if (active) {
-        f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const u32x4 aq = lds_read16(Qs + (qh * 32 + l32) * QSTR + 16 * ks + 8 * h32);
-          const u32x4 bk = lds_read16(Ks + (kbw * 32 + l32) * KSTR + 16 * ks + 8 * h32);
-          s = Elem<T>::mfma(aq, bk, s);
-          const u32x4 ad = lds_read16(Ds + (qh * 32 + l32) * QSTR + 16 * ks + 8 * h32);
-          const u32x4 bv = lds_read16(Vs + (kbw * 32 + l32) * KSTR + 16 * ks + 8 * h32);
-          dp = Elem<T>::mfma(ad, bv, dp);
-        }
-        // S layout: lane = key, register r = query row 8 (r/4) + 4 h + r % 4.
-        const bool need_mask = (qw0 + 32 > p.Sq) || !key_ok || (CAUSAL && qw0 < k0 + kbw * 32 + 31);
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int rl = qh * 32 + 8 * g4 + 4 * h32;
-          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&rowstat[buf][0][rl]);
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&rowstat[buf][1][rl]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * g4 + e;
-            float x = fmaf(s[r], p.scale_log2, -l4[e]);
-            if (need_mask) {
-              const int qi = qw0 + 8 * g4 + 4 * h32 + e;
-              x = (qi < p.Sq && key_ok && (!CAUSAL || key <= qi)) ? x : kNegInf;
-            }
-            const float pv = fast_exp2(x);
-            s[r] = pv;
-            dp[r] = pv * (dp[r] - d4[e]);
-          }
-        }
-        const u32x4 p0 = pack8<T>(s, 0), p1 = pack8<T>(s, 8);
-        const u32x4 s0 = pack8<T>(dp, 0), s1 = pack8<T>(dp, 8);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          u32x4 a = lds_read_tr_operand(Ds, QSTR, qh * 32, 32 * db, lane);
-          dv[db] = Elem<T>::mfma(a, p0, dv[db]);
-          a = lds_read_tr_operand(Ds, QSTR, qh * 32 + 16, 32 * db, lane);
-          dv[db] = Elem<T>::mfma(a, p1, dv[db]);
-          a = lds_read_tr_operand(Qs, QSTR, qh * 32, 32 * db, lane);
-          dk[db] = Elem<T>::mfma(a, s0, dk[db]);
-          a = lds_read_tr_operand(Qs, QSTR, qh * 32 + 16, 32 * db, lane);
-          dk[db] = Elem<T>::mfma(a, s1, dk[db]);
-        }
-      }
+      // Causal: a unit that reaches above the diagonal for this wave's keys is
+      // masked (key <= row); the few units entirely above it (the first
+      // query tile for the upper waves) are computed fully masked rather than
+      // branched around, which keeps the loop body one block. Rows >= Sq and
+      // keys >= Sk need no mask: their Q/dO (K/V) rows load as zeros and their
+      // LSE/delta as 0, so they add nothing to any valid dK/dV row.
+      unit(Qs, Ds, buf, qrow0, qrow0 < kw0 + 31);
       if (it + 1 < ub) sstore(buf ^ 1);
       __syncthreads();
     }
 
-    // Flush: waves of query half 1 hand their sums to half 0 through LDS
-    // (dK in the Q/dO stages, dV in the K/V tiles), which stores the tile.
-    float* rk = reinterpret_cast<float*>(Qstage);
-    float* rv = reinterpret_cast<float*>(smem);
-    if (qh == 1) {
+    // Flush: dK^T / dV^T layout is lane = key, register r = head_dim
+    // 32 db + 8 (r/4) + 4 h + r % 4. A tile this workgroup covered alone is
+    // final; a shared one goes to this workgroup's partial slot.
+    const bool full = ua == 0 && ub == per_tile;
+    float* slot = p.part + (int64_t)(2 * blockIdx.x + (first_seg ? 0 : 1)) * 2 * kBNK * DT;
+    uint16_t* Dk = p.dk + b * p.dk_sb + kvh * p.dk_sh + key * p.dk_ss;
+    uint16_t* Dv = p.dv + b * p.dv_sb + kvh * p.dv_sh + key * p.dv_ss;
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
+    for (int db = 0; db < NDB; ++db) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int d = 32 * db + 8 * (r >> 2) + 4 * h32 + (r & 3);
-          rk[(kbw * 32 + l32) * RSTR + d] = dk[db][r];
-          rv[(kbw * 32 + l32) * RSTR + d] = dv[db][r];
-        }
-      }
-    }
-    __syncthreads();
-    if (qh == 0) {
-      const bool full = ua == 0 && ub == per_tile;
-      float* slot = p.part + (int64_t)(2 * blockIdx.x + (first_seg ? 0 : 1)) * 2 * kBNK * DT;
-      uint16_t* Dk = p.dk + b * p.dk_sb + kvh * p.dk_sh + key * p.dk_ss;
-      uint16_t* Dv = p.dv + b * p.dv_sb + kvh * p.dv_sh + key * p.dv_ss;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int d = 32 * db + 8 * g4 + 4 * h32;
-          float kk[4], vv[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            kk[e] = (dk[db][4 * g4 + e] + rk[(kbw * 32 + l32) * RSTR + d + e]) * p.scale;
-            vv[e] = dv[db][4 * g4 + e] + rv[(kbw * 32 + l32) * RSTR + d + e];
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = 32 * db + 8 * g4 + 4 * h32;
+        const int r = 4 * g4;
+        if (full) {
+          if (key_ok && d < p.D) {
+            u32x2 w;
+            w[0] = pack2<T>(dk[db][r] * p.scale, dk[db][r + 1] * p.scale);
+            w[1] = pack2<T>(dk[db][r + 2] * p.scale, dk[db][r + 3] * p.scale);
+            *reinterpret_cast<u32x2*>(Dk + d) = w;
+            w[0] = pack2<T>(dv[db][r], dv[db][r + 1]);
+            w[1] = pack2<T>(dv[db][r + 2], dv[db][r + 3]);
+            *reinterpret_cast<u32x2*>(Dv + d) = w;
           }
-          if (full) {
-            if (key_ok && d < p.D) {
-              u32x2 w;
-              w[0] = pack2<T>(kk[0], kk[1]);
-              w[1] = pack2<T>(kk[2], kk[3]);
-              *reinterpret_cast<u32x2*>(Dk + d) = w;
-              w[0] = pack2<T>(vv[0], vv[1]);
-              w[1] = pack2<T>(vv[2], vv[3]);
-              *reinterpret_cast<u32x2*>(Dv + d) = w;
-            }
-          } else {
-            float* sk = slot + (kbw * 32 + l32) * DT + d;
-            *reinterpret_cast<float4*>(sk) = make_float4(kk[0], kk[1], kk[2], kk[3]);
-            *reinterpret_cast<float4*>(sk + kBNK * DT) = make_float4(vv[0], vv[1], vv[2], vv[3]);
-          }
+        } else {
+          float* sk = slot + (wave * 32 + l32) * DT + d;
+          *reinterpret_cast<float4*>(sk) =
+              make_float4(dk[db][r] * p.scale, dk[db][r + 1] * p.scale, dk[db][r + 2] * p.scale,
+                          dk[db][r + 3] * p.scale);
+          *reinterpret_cast<float4*>(sk + kBNK * DT) =
+              make_float4(dv[db][r], dv[db][r + 1], dv[db][r + 2], dv[db][r + 3]);
         }
       }
     }
@@ -616,9 +666,9 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
     p.nkt = cdiv(p.Sk, kBNK);
     p.units = dkdv_total_units(p.ngroups, p.G, p.nqt, p.nkt, causal);
     if (causal)
-      hipLaunchKernelGGL((dkdv_kernel<T, DT, true>), dim3((unsigned)p.nwg), dim3(512), 0, stream, p);
+      hipLaunchKernelGGL((dkdv_kernel<T, DT, true>), dim3((unsigned)p.nwg), dim3(256), 0, stream, p);
     else
-      hipLaunchKernelGGL((dkdv_kernel<T, DT, false>), dim3((unsigned)p.nwg), dim3(512), 0, stream, p);
+      hipLaunchKernelGGL((dkdv_kernel<T, DT, false>), dim3((unsigned)p.nwg), dim3(256), 0, stream, p);
     int rc = check_launch("kf_attn_bwd(dkdv)");
     if (rc) return rc;
   }
