@@ -2,7 +2,9 @@
 //
 // Launches on one stream, no atomics, deterministic:
 //   1. delta_kernel: delta[i] = sum_d O[i,d] * dO[i,d] from the stored
-//      low-precision O (reference triton_backward.py:45).
+//      low-precision O (reference triton_backward.py:45), stored negated,
+//      and LSE[i] log2(e), for the dK/dV kernel, which loads both rows
+//      straight into LDS and starts its dP accumulators at -delta.
 //   2. dq_kernel (query-stationary, same layout as the forward, two waves per
 //      SIMD): per key tile it recomputes S^T = K Q^T and dP^T = V dO^T, forms
 //      dS^T = P^T (dP^T - delta) with P = exp(scale S - LSE), and accumulates
@@ -40,7 +42,8 @@ struct BwdParams {
   const uint16_t* o;
   const uint16_t* dout;
   const float* lse;
-  float* delta;
+  float* delta;  // -rowsum(O * dO), written by delta_kernel
+  float* lse2;   // LSE * log2(e), written by delta_kernel
   float* part;  // dK/dV fp32 partials: [2 * nwg][2][128][DT]
   uint16_t* dq;
   uint16_t* dk;
@@ -108,7 +111,10 @@ __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
   acc += __shfl_xor(acc, 4);
   acc += __shfl_xor(acc, 2);
   acc += __shfl_xor(acc, 1);
-  if (c16 == 0 && row < total) p.delta[row] = acc;
+  if (c16 == 0 && row < total) {
+    p.delta[row] = -acc;
+    p.lse2[row] = p.lse[row] * kLog2e;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -171,7 +177,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
   }
   const int64_t rowlin = ((int64_t)b * p.Hq + h) * p.Sq + qrow;
   const float lse2 = row_ok ? p.lse[rowlin] * kLog2e : 0.f;
-  const float dlt = row_ok ? p.delta[rowlin] : 0.f;
+  const float dlt = row_ok ? -p.delta[rowlin] : 0.f;  // the workspace holds -delta
 
   f32x16 dq[NDB];
 #pragma unroll
@@ -282,23 +288,28 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
 // accumulators live in accumulation registers). Wave w owns keys
 // 32 w .. 32 w + 31 of the 128-key tile and keeps their K and V rows in
 // registers as MFMA B operands for the whole tile; per unit it covers all 64
-// query rows, which the workgroup stages (Q, dO, LSE, delta) through LDS,
-// double-buffered. Per unit and 32-row query block:
+// query rows. The unit's Q and dO tiles and its LSE / delta rows are loaded
+// straight into LDS (no register staging) in a ring of NST stages, issued two
+// units ahead. Per unit and 32-row query block:
 //   S  = Q K^T,  dP = dO V^T            (A = Q / dO rows from LDS, B = K / V)
 //   P  = exp2(scale log2e S - LSE log2e),  dS = P (dP - delta)
 //   dV^T += dO^T P,  dK^T += Q^T dS      (A = transposed LDS reads, B = P / dS
 //                                         straight from the S / dP registers)
 template <typename T, int DT, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
-  constexpr int QSTR = DT + 16;  // Q/dO tiles: b128 and transposed reads
-  constexpr int QT = kBMQ * QSTR;
   constexpr int CPR = DT / 8;
-  constexpr int QCPT = kBMQ * CPR / 256;  // 16-byte chunks per thread of a Q (or dO) tile
+  constexpr int QT = kBMQ * DT;        // elements of one Q (or dO) tile
+  constexpr int NQI = CPR / 4;         // 1 KB DMA instructions per wave per tile
+  constexpr int NST = 3;               // LDS ring stages
   constexpr int NKS = DT / 16;
   constexpr int NDB = DT / 32;
-  static_assert(kBMQ * CPR % 256 == 0, "Q tile chunks must divide over the workgroup");
-  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * QT];        // [buf][Q | dO]
-  __shared__ __attribute__((aligned(16))) float rowstat[2][2][kBMQ];   // [buf][lse2, delta][row]
+  using Tile = SwizzledTile<CPR>;
+  static_assert(kBMQ * CPR == 4 * 64 * NQI, "tile chunks must split into whole DMA instructions");
+  __shared__ __attribute__((aligned(16))) uint16_t stage[NST][2][QT];   // [stage][Q | dO]
+  // [stage][lse2, delta, (unused x2)][row]: waves 2 and 3 also issue a
+  // (zero-filling) statistics load into the unused rows, so that every wave
+  // runs the same instruction stream and vmcnt count.
+  __shared__ __attribute__((aligned(16))) float rowstat[NST][4][kBMQ];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
@@ -310,8 +321,6 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
   if (u >= uend) return;
 
   f32x16 dk[NDB], dv[NDB];
-  u32x4 qreg[QCPT], dreg[QCPT];
-  float st_l = 0.f, st_d = 0.f;
 
   int kt = 0;
   int64_t row_base = 0;  // first unit of key-tile row kt
@@ -336,6 +345,10 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
     const int key = kw0 + l32;
     const bool key_ok = key < p.Sk;
 
+    // Stages of the previous segment (and its flush stores) are done with.
+    wait_all_memory();
+    __syncthreads();
+
     // This wave's K and V rows as B operands: lane = key, slots = head_dim.
     u32x4 kf[NKS], vf[NKS];
     {
@@ -354,101 +367,158 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
       dk[db] = zero16();
       dv[db] = zero16();
     }
+    // K/V fragments are in registers before the ring starts: the ring's own
+    // loads are waited for explicitly below, and any compiler-inserted wait
+    // on these fragments inside the loop would also drain the ring.
+    wait_all_memory();
 
-    auto gload = [&](int it) {
-      const int g = it / nq;
-      const int qt = qs + (it - g * nq);
-      const int h = kvh * p.G + g;
-      const int qbase = qt * kBMQ;
-      const auto qr = make_rsrc(p.q + b * p.q_sb + h * p.q_sh, rows_extent(p.Sq, p.q_ss, p.D));
-      const auto dor = make_rsrc(p.dout + b * p.do_sb + h * p.do_sh, rows_extent(p.Sq, p.do_ss, p.D));
+    // Per-lane DMA plan, fixed for the segment: for each of this wave's NQI
+    // 1 KB blocks of a tile, the tile row this lane fills (or a huge value
+    // when its chunk is head-dim padding, so the row test below fails) and
+    // the byte offset of its chunk within the row.
+    int dma_row[NQI];
+    uint32_t dma_col[NQI];
 #pragma unroll
-      for (int c = 0; c < QCPT; ++c) {
-        const int e = tid + 256 * c;
-        const int row = e / CPR, col = e % CPR;
-        const int qi = qbase + row;
-        const bool ok = qi < p.Sq && col * 8 < p.D;
-        qreg[c] = buf_load16(qr, ok ? (uint32_t)(qi * p.q_ss + col * 8) * 2u : kOOB);
-        dreg[c] = buf_load16(dor, ok ? (uint32_t)(qi * p.do_ss + col * 8) * 2u : kOOB);
-      }
-      if (tid < kBMQ) {
-        const int qi = qbase + tid;
-        const int64_t rl = ((int64_t)b * p.Hq + h) * p.Sq + qi;
-        // Raw values here; the scaling waits until sstore so that issuing
-        // the loads never waits for them.
-        st_l = qi < p.Sq ? p.lse[rl] : 0.f;
-        st_d = qi < p.Sq ? p.delta[rl] : 0.f;
+    for (int k = 0; k < NQI; ++k) {
+      const int pc = (wave * NQI + k) * 64 + lane;  // physical chunk this lane fills
+      const int r = pc / CPR;
+      const int c = (pc % CPR) ^ (r & (Tile::SW - 1));
+      dma_row[k] = c * 8 < p.D ? r : 0x7fffffff;
+      dma_col[k] = (uint32_t)c * 16u;
+    }
+    // Units are walked in order (query head g, query tile qt): `Walk`
+    // advances one unit without divisions.
+    struct Walk {
+      int g, qt;
+    };
+    auto walk_init = [&](int it) {
+      Walk w;
+      w.g = it / nq;
+      w.qt = qs + (it - w.g * nq);
+      return w;
+    };
+    auto walk_next = [&](Walk& w) {
+      if (++w.qt == qs + nq) {
+        w.qt = qs;
+        ++w.g;
       }
     };
-    auto sstore = [&](int buf) {
-      uint16_t* Qs = smem + buf * 2 * QT;
-      uint16_t* Ds = Qs + QT;
-#pragma unroll
-      for (int c = 0; c < QCPT; ++c) {
-        const int e = tid + 256 * c;
-        const int row = e / CPR, col = e % CPR;
-        lds_write16(Qs + row * QSTR + col * 8, qreg[c]);
-        lds_write16(Ds + row * QSTR + col * 8, dreg[c]);
-      }
-      if (tid < kBMQ) {
-        rowstat[buf][0][tid] = st_l * kLog2e;
-        rowstat[buf][1][tid] = st_d;
+    constexpr int NDMA = 2 * NQI + 1;  // DMA instructions per unit (the last: LSE or delta rows)
+    struct Dma {
+      __amdgpu_buffer_rsrc_t qr, dor, sr;
+      int qbase, st;
+    };
+    // A unit past the segment's end gets an out-of-range row base: its loads
+    // then only deposit zeros into the (free) stage, which keeps the issue
+    // unconditional.
+    auto dma_setup = [&](const Walk& w, int st, bool real) {
+      Dma d;
+      const int h = kvh * p.G + (real ? w.g : 0);
+      d.qbase = real ? w.qt * kBMQ : (1 << 29);
+      d.st = st;
+      d.qr = make_rsrc(p.q + b * p.q_sb + h * p.q_sh, rows_extent(p.Sq, p.q_ss, p.D));
+      d.dor = make_rsrc(p.dout + b * p.do_sb + h * p.do_sh, rows_extent(p.Sq, p.do_ss, p.D));
+      const int64_t rb = ((int64_t)b * p.Hq + h) * p.Sq;
+      d.sr = make_rsrc(wave == 0 ? p.lse2 + rb : p.delta + rb, (uint32_t)p.Sq * 4u);
+      return d;
+    };
+    // DMA instruction j of a unit: Q / dO blocks, then the row statistics.
+    auto dma_issue = [&](const Dma& d, int j) {
+      if (j < 2 * NQI) {
+        const int k = j >> 1;
+        const bool isq = (j & 1) == 0;
+        const bool ok = dma_row[k] < p.Sq - d.qbase;
+        const uint32_t ss = (uint32_t)(isq ? p.q_ss : p.do_ss) * 2u;
+        const uint32_t off = ok ? (uint32_t)(d.qbase + dma_row[k]) * ss + dma_col[k] : kOOB;
+        dma16(isq ? d.qr : d.dor, &stage[d.st][isq ? 0 : 1][(wave * NQI + k) * 512], off);
+      } else {
+        const int qi = d.qbase + lane;
+        dma4(d.sr, &rowstat[d.st][wave][0], wave < 2 && qi < p.Sq ? (uint32_t)qi * 4u : kOOB);
       }
     };
 
     // One unit: both 32-row query blocks (qb) of the staged tile against this
-    // wave's 32 keys. With `diag` the causal mask (key <= row) is applied;
-    // otherwise its comparison is made to pass for every element (one body
-    // for both cases keeps the register footprint of a single copy).
+    // wave's 32 keys, with the causal mask (key <= row) on blocks that cross
+    // the diagonal for this wave's keys.
     //
     // With one wave per SIMD nothing else hides latency, so the unit is
-    // software-pipelined by hand and the order pinned with scheduling fences:
-    //   phase 1: S/dP MFMAs of qb 0       | LDS operand reads of qb 1
-    //   phase 2: S/dP MFMAs of qb 1       | softmax of qb 0, transposed reads of qb 0
-    //   phase 3: dV/dK MFMAs of qb 0      | softmax of qb 1, transposed reads of qb 1
-    //   phase 4: dV/dK MFMAs of qb 1
-    // The MFMAs run on the matrix core while the interleaved VALU and LDS
-    // instructions of the same wave issue.
-    auto unit = [&](const uint16_t* Qs, const uint16_t* Ds, int buf, int qrow0, bool diag) {
+    // software-pipelined by hand as one stream of MFMA slots, the order pinned
+    // with scheduling fences:
+    //   slots [0, NSD)          S/dP MFMAs of qb 0
+    //   slots [NSD, 2 NSD)      S/dP MFMAs of qb 1      + softmax of qb 0
+    //   slots [2 NSD, +NVK)     dV/dK MFMAs of qb 0     + softmax of qb 1
+    //   slots [.., +NVK)        dV/dK MFMAs of qb 1
+    // (NSD = NVK = 16 at head_dim 128; smaller tiles run several softmax
+    // elements per slot.)
+    // Each slot also issues the LDS read of the operand LA slots ahead (a
+    // short window keeps few operand registers live) and, spread over the
+    // middle slots, the DMA of unit + 2. The MFMAs run on the matrix core
+    // while the interleaved VALU, LDS and memory instructions issue.
+    auto unit = [&](int st, int qrow0, const Dma& nd) {
+      const uint16_t* Qs = stage[st][0];
+      const uint16_t* Ds = stage[st][1];
       constexpr int NSD = 2 * NKS;  // S/dP MFMAs per block
       constexpr int NVK = 4 * NDB;  // dV/dK MFMAs per block
-      u32x4 aop[2][NSD];            // S/dP A operands: [2 ks] = Q, [2 ks + 1] = dO
-      u32x4 top[2][NVK];            // dV/dK A operands: [4 db + j], j = dO lo/hi, Q lo/hi
+      constexpr int NSLOT = 2 * NSD + 2 * NVK;
+      constexpr int LA = 4;         // operand read-ahead, in slots
+      u32x4 op[NSLOT];              // A operand of every slot (short live ranges)
       f32x16 s[2], dp[2];
       f32x4 l4[2][4], d4[2][4];
       u32x4 pk[2][4];               // P lo/hi, dS lo/hi
-      int t[2];
 
-      auto read_sd = [&](int qb, int i) {
-        const int ks = i >> 1;
-        const uint16_t* base = (i & 1) ? Ds : Qs;
-        aop[qb][i] = lds_read16(base + (qb * 32 + l32) * QSTR + 16 * ks + 8 * h32);
+      // Slot m -> (kind, block, index): kind 0 = S/dP, 1 = dV/dK.
+      auto read_op = [&](int m) {
+        if (m < 2 * NSD) {
+          const int qb = m / NSD, i = m % NSD, ks = i >> 1;
+          op[m] = lds_read16(((i & 1) ? Ds : Qs) + Tile::chunk(qb * 32 + l32, 2 * ks + h32) * 8);
+        } else {
+          const int qb = (m - 2 * NSD) / NVK, j = (m - 2 * NSD) % NVK;
+          const int db = j % NDB, w = j / NDB;  // w: dV lo, dK lo, dV hi, dK hi
+          const bool isv = (w & 1) == 0;
+          op[m] = lds_read_tr_operand_sw<CPR>(isv ? Ds : Qs, qb * 32 + 16 * (w >> 1), 32 * db, lane);
+        }
       };
-      auto mfma_sd = [&](int qb, int i) {
-        const int ks = i >> 1;
-        if (i & 1)
-          dp[qb] = Elem<T>::mfma(aop[qb][i], vf[ks], dp[qb]);
-        else
-          s[qb] = Elem<T>::mfma(aop[qb][i], kf[ks], s[qb]);
+      auto mfma_slot = [&](int m) {
+        if (m < 2 * NSD) {
+          const int qb = m / NSD, i = m % NSD, ks = i >> 1;
+          if (i & 1)
+            dp[qb] = Elem<T>::mfma(op[m], vf[ks], dp[qb]);
+          else
+            s[qb] = Elem<T>::mfma(op[m], kf[ks], s[qb]);
+        } else {
+          const int qb = (m - 2 * NSD) / NVK, j = (m - 2 * NSD) % NVK;
+          const int db = j % NDB, w = j / NDB;
+          // pk layout: [0] P lo, [1] P hi, [2] dS lo, [3] dS hi
+          const int src = (w & 1) ? 2 + (w >> 1) : (w >> 1);
+          if ((w & 1) == 0)
+            dv[db] = Elem<T>::mfma(op[m], pk[qb][src], dv[db]);
+          else
+            dk[db] = Elem<T>::mfma(op[m], pk[qb][src], dk[db]);
+        }
       };
       auto read_stats = [&](int qb) {
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           const int rl = qb * 32 + 8 * g4 + 4 * h32;
-          l4[qb][g4] = *reinterpret_cast<const f32x4*>(&rowstat[buf][0][rl]);
-          d4[qb][g4] = *reinterpret_cast<const f32x4*>(&rowstat[buf][1][rl]);
+          l4[qb][g4] = *reinterpret_cast<const f32x4*>(&rowstat[st][0][rl]);
+          d4[qb][g4] = *reinterpret_cast<const f32x4*>(&rowstat[st][1][rl]);
         }
-        // key <= row  <=>  key - (block row 0) - 4 h <= 8 (r/4) + r % 4
-        t[qb] = CAUSAL && diag ? key - (qrow0 + 32 * qb) - 4 * h32 : -(1 << 30);
       };
       // S layout: lane = key, register r = query row 8 (r/4) + 4 h + r % 4.
+      // Causal mask of block qb: key <= row  <=>  t <= 8 (r/4) + r % 4 with
+      // t = key - (block row 0) - 4 h; blocks clear of the diagonal get a t
+      // that passes every comparison (branch-free: one body for all units).
+      int t[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+        t[qb] = CAUSAL && qrow0 + 32 * qb < kw0 + 31 ? key - (qrow0 + 32 * qb) - 4 * h32 : -(1 << 30);
       auto soft = [&](int qb, int r) {
         const int g4 = r >> 2, e = r & 3;
         float x = fmaf(s[qb][r], p.scale_log2, -l4[qb][g4][e]);
         if (CAUSAL) x = t[qb] <= 8 * g4 + e ? x : kNegInf;
         const float pv = fast_exp2(x);
         s[qb][r] = pv;
-        dp[qb][r] = pv * (dp[qb][r] - d4[qb][g4][e]);
+        dp[qb][r] = pv * dp[qb][r];  // dP accumulated from -delta: dS = P (dP - delta)
         if (r == 7) {
           pk[qb][0] = pack8<T>(s[qb], 0);
           pk[qb][2] = pack8<T>(dp[qb], 0);
@@ -457,75 +527,77 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
           pk[qb][3] = pack8<T>(dp[qb], 8);
         }
       };
-      auto read_tr = [&](int qb, int j) {
-        const int db = j >> 2, w = j & 3;
-        top[qb][j] = lds_read_tr_operand((w < 2) ? Ds : Qs, QSTR, qb * 32 + 16 * (w & 1), 32 * db, lane);
-      };
-      auto mfma_vk = [&](int qb, int j) {
-        const int db = j >> 2, w = j & 3;
-        if (w < 2)
-          dv[db] = Elem<T>::mfma(top[qb][j], pk[qb][w], dv[db]);
-        else
-          dk[db] = Elem<T>::mfma(top[qb][j], pk[qb][w], dk[db]);
-      };
 
-      s[0] = s[1] = dp[0] = dp[1] = zero16();
-#pragma unroll
-      for (int i = 0; i < NSD; ++i) read_sd(0, i);
+      s[0] = s[1] = zero16();
       read_stats(0);
       read_stats(1);
+      // dP accumulators start at -delta of their rows (register r <-> row
+      // 8 (r/4) + 4 h + r % 4, the layout of d4), so dS = P * dP needs no
+      // subtraction.
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dp[qb][r] = d4[qb][r >> 2][r & 3];
+      static_for<0, LA>([&](auto mc) { read_op(decltype(mc)::value); });
       __builtin_amdgcn_sched_barrier(0);
-      // phase 1
-#pragma unroll
-      for (int i = 0; i < NSD; ++i) {
-        mfma_sd(0, i);
-        read_sd(1, i);
+      // The softmax of block 0 runs in the S/dP slots of block 1 and that of
+      // block 1 in the dV/dK slots of block 0: each finishes before the first
+      // MFMA that consumes its P/dS. EPS* elements per slot fit 16 in a phase.
+      constexpr int EPS0 = (16 + NSD - 1) / NSD;
+      constexpr int EPS1 = (16 + NVK - 1) / NVK;
+      constexpr int DMA0 = NSD;                 // first slot carrying a DMA
+      constexpr int DMAS = (2 * NSD + NVK - DMA0) / NDMA;  // slot spacing
+      static_assert(DMAS >= 1, "every DMA instruction gets a slot");
+      static_for<0, NSLOT>([&](auto mc) {
+        constexpr int m = decltype(mc)::value;
+        mfma_slot(m);
+        if constexpr (m + LA < NSLOT) read_op(m + LA);
+        if constexpr (m >= NSD && m < 2 * NSD) {
+          static_for<0, EPS0>([&](auto ec) {
+            constexpr int r = (m - NSD) * EPS0 + decltype(ec)::value;
+            if constexpr (r < 16) soft(0, r);
+          });
+        }
+        if constexpr (m >= 2 * NSD && m < 2 * NSD + NVK) {
+          static_for<0, EPS1>([&](auto ec) {
+            constexpr int r = (m - 2 * NSD) * EPS1 + decltype(ec)::value;
+            if constexpr (r < 16) soft(1, r);
+          });
+        }
+        if constexpr (m >= DMA0 && (m - DMA0) % DMAS == 0 && (m - DMA0) / DMAS < NDMA)
+          dma_issue(nd, (m - DMA0) / DMAS);
         __builtin_amdgcn_sched_barrier(0);
-      }
-      // phase 2
-      constexpr int P2 = NSD > 16 ? NSD : 16;
-#pragma unroll
-      for (int i = 0; i < P2; ++i) {
-        if (i < NSD) mfma_sd(1, i);
-        if (i < 16) soft(0, i);
-        if (i < NVK) read_tr(0, i);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // phase 3
-      constexpr int P3 = NVK > 16 ? NVK : 16;
-#pragma unroll
-      for (int i = 0; i < P3; ++i) {
-        if (i < NVK) mfma_vk(0, i);
-        if (i < 16) soft(1, i);
-        if (i < NVK) read_tr(1, i);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // phase 4
-#pragma unroll
-      for (int i = 0; i < NVK; ++i) mfma_vk(1, i);
+      });
     };
 
-    __syncthreads();  // every wave is done with the previous segment's stages
-    gload(ua);
-    sstore(0);
-    wait_all_memory();
-    __syncthreads();
+    // Ring: at the top of unit `it` the loads of units it and it + 1 are in
+    // flight; wait for those of `it` (this wave's), then the barrier makes
+    // every wave's loads visible and frees the stage of unit it - 1, which
+    // receives unit it + 2 (issued from inside the unit's first phase).
+    Walk wcur = walk_init(ua), wdma = wcur;
+    {
+      const Dma d0 = dma_setup(wdma, 0, true);
+#pragma unroll
+      for (int j = 0; j < NDMA; ++j) dma_issue(d0, j);
+      walk_next(wdma);
+      const Dma d1 = dma_setup(wdma, 1, ua + 1 < ub);
+#pragma unroll
+      for (int j = 0; j < NDMA; ++j) dma_issue(d1, j);
+      walk_next(wdma);
+    }
+    int st = 0;
     for (int it = ua; it < ub; ++it) {
-      const int buf = (it - ua) & 1;
-      if (it + 1 < ub) gload(it + 1);
-      const int g = it / nq;
-      const int qrow0 = (qs + (it - g * nq)) * kBMQ;  // first query row of the unit
-      const uint16_t* Qs = smem + buf * 2 * QT;
-      const uint16_t* Ds = Qs + QT;
-      // Causal: a unit that reaches above the diagonal for this wave's keys is
-      // masked (key <= row); the few units entirely above it (the first
-      // query tile for the upper waves) are computed fully masked rather than
-      // branched around, which keeps the loop body one block. Rows >= Sq and
-      // keys >= Sk need no mask: their Q/dO (K/V) rows load as zeros and their
-      // LSE/delta as 0, so they add nothing to any valid dK/dV row.
-      unit(Qs, Ds, buf, qrow0, qrow0 < kw0 + 31);
-      if (it + 1 < ub) sstore(buf ^ 1);
+      KF_WAIT_VMCNT(NDMA);  // unit it + 1's loads may still be in flight
       __syncthreads();
+      const Dma nd = dma_setup(wdma, st == 0 ? NST - 1 : st - 1, it + 2 < ub);
+      // Rows >= Sq and keys >= Sk need no mask: their Q/dO (K/V) rows load as
+      // zeros and their LSE/delta as 0, so they add nothing to any valid dK/dV
+      // row. A unit entirely above the causal diagonal for this wave is
+      // computed fully masked rather than branched around.
+      unit(st, wcur.qt * kBMQ, nd);
+      walk_next(wcur);
+      walk_next(wdma);
+      st = st == NST - 1 ? 0 : st + 1;
     }
 
     // Flush: dK^T / dV^T layout is lane = key, register r = head_dim
@@ -705,7 +777,7 @@ extern "C" size_t kf_attn_bwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv
                                               int64_t Sk, int64_t D, int causal) {
   (void)Hkv; (void)Sk; (void)causal;
   if (B <= 0 || Hq <= 0 || Sq <= 0 || D <= 0) return 0;
-  return delta_bytes(B, Hq, Sq) + partial_bytes(device_cu_count(), D);
+  return 2 * delta_bytes(B, Hq, Sq) + partial_bytes(device_cu_count(), D);
 }
 
 extern "C" int kf_attn_bwd_stages(int stages, const void* q, const void* k, const void* v,
@@ -743,7 +815,8 @@ extern "C" int kf_attn_bwd_stages(int stages, const void* q, const void* k, cons
   p.o = (const uint16_t*)o; p.dout = (const uint16_t*)dout; p.lse = lse;
   p.delta = (float*)workspace;
   p.nwg = device_cu_count();
-  p.part = (float*)((char*)workspace + delta_bytes(B, Hq, Sq));
+  p.lse2 = (float*)((char*)workspace + delta_bytes(B, Hq, Sq));
+  p.part = (float*)((char*)workspace + 2 * delta_bytes(B, Hq, Sq));
   p.dq = (uint16_t*)dq; p.dk = (uint16_t*)dk; p.dv = (uint16_t*)dv;
   p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
   p.k_sb = k_strides[0]; p.k_sh = k_strides[1]; p.k_ss = k_strides[2];

@@ -22,7 +22,20 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace kf {
+
+// Compile-time loop: calls f(std::integral_constant<int, I>) for I in [B, E).
+// Used where every iteration must see its index as a constant (register
+// arrays indexed by it stay in registers).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -159,6 +172,73 @@ __device__ inline u32x4 lds_read_tr_operand(const uint16_t* tile, int stride, in
   const uint16_t* base = tile + (row0 + 4 * h + (p >> 2)) * stride + col0 + 16 * g + 4 * (p & 3);
   u32x2 lo = lds_read_tr16(base);
   u32x2 hi = lds_read_tr16(base + 8 * stride);
+  u32x4 out = {lo[0], lo[1], hi[0], hi[1]};
+  return out;
+}
+
+// Direct-to-LDS buffer loads (gfx950): every lane reads `size` bytes at its own
+// byte offset and the data lands at lds_base + size * lane, with lds_base
+// wave-uniform (M0). Checked on the device with an in-bounds probe. Offsets
+// beyond the resource extent (kOOB) deposit zeros, like register loads.
+//
+// They are issued as inline assembly on purpose: the compiler cannot tell
+// which LDS bytes an in-flight load of this kind writes, so for the builtin it
+// waits for all of them (vmcnt(0)) before any later LDS read, which would
+// drain a multi-stage ring every step. Callers therefore wait for these loads
+// themselves (KF_WAIT_VMCNT + barrier). The compiler's own waits on other
+// vector-memory loads stay correct: the counter completes in order, so extra
+// younger loads it does not know of only make its waits longer.
+__device__ inline uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const KF_LDS void*)p;
+}
+__device__ inline void dma16(__amdgpu_buffer_rsrc_t r, uint16_t* lds_base, uint32_t byte_off) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds_base))), "v"(byte_off), "s"(r)
+      : "memory", "m0");
+}
+__device__ inline void dma4(__amdgpu_buffer_rsrc_t r, float* lds_base, uint32_t byte_off) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dword %1, %2, 0 offen lds"
+      :
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds_base))), "v"(byte_off), "s"(r)
+      : "memory", "m0");
+}
+
+// s_waitcnt that waits until at most n vector-memory operations of the wave
+// are outstanding (gfx9 encoding: vmcnt bits [3:0] and [15:14], expcnt and
+// lgkmcnt left at their maxima). n must be a compile-time constant < 64.
+#define KF_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt((((n) & 15) | ((((n) >> 4) & 3) << 14) | (7 << 4) | (15 << 8)))
+
+// Row-major 16-bit tile of `rows` x (8 cpr) elements stored without padding,
+// 16-byte chunks XOR-swizzled within each row: logical chunk c of row r lives
+// at physical chunk c ^ (r & (sw - 1)), sw the largest power of two (<= 16)
+// dividing cpr. Consecutive rows read at the same logical column then fall on
+// different banks.
+template <int CPR>
+struct SwizzledTile {
+  static constexpr int SW = (CPR % 16 == 0) ? 16 : (CPR % 8 == 0) ? 8 : 4;
+  __device__ static inline int chunk(int r, int c) { return r * CPR + (c ^ (r & (SW - 1))); }
+  // Element offset of element col (any in [0, 8 cpr)) of row r.
+  __device__ static inline int elem(int r, int col) { return chunk(r, col >> 3) * 8 + (col & 7); }
+};
+
+// Transposed MFMA A operand (as lds_read_tr_operand) from a swizzled tile.
+template <int CPR>
+__device__ inline u32x4 lds_read_tr_operand_sw(const uint16_t* tile, int row0, int col0, int lane) {
+  const int p = lane & 15;
+  const int h = lane >> 5;
+  const int g = (lane >> 4) & 1;
+  const int r = row0 + 4 * h + (p >> 2);
+  const int col = col0 + 16 * g + 4 * (p & 3);
+  u32x2 lo = lds_read_tr16(tile + SwizzledTile<CPR>::elem(r, col));
+  u32x2 hi = lds_read_tr16(tile + SwizzledTile<CPR>::elem(r + 8, col));
   u32x4 out = {lo[0], lo[1], hi[0], hi[1]};
   return out;
 }
