@@ -507,7 +507,8 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
       // S layout: lane = key, register r = query row 8 (r/4) + 4 h + r % 4.
       // Causal mask of block qb: key <= row  <=>  t <= 8 (r/4) + r % 4 with
       // t = key - (block row 0) - 4 h; blocks clear of the diagonal get a t
-      // that passes every comparison (branch-free: one body for all units).
+      // that passes every comparison (branch-free: one body for all units;
+      // two specialised bodies exceed the register budget).
       int t[2];
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb)
@@ -528,16 +529,17 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
         }
       };
 
-      s[0] = s[1] = zero16();
-      read_stats(0);
-      read_stats(1);
       // dP accumulators start at -delta of their rows (register r <-> row
       // 8 (r/4) + 4 h + r % 4, the layout of d4), so dS = P * dP needs no
-      // subtraction.
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
+      // subtraction. Block 1's statistics are read a few slots before its
+      // first MFMA.
+      auto init_block = [&](int qb) {
+        read_stats(qb);
+        s[qb] = zero16();
 #pragma unroll
         for (int r = 0; r < 16; ++r) dp[qb][r] = d4[qb][r >> 2][r & 3];
+      };
+      init_block(0);
       static_for<0, LA>([&](auto mc) { read_op(decltype(mc)::value); });
       __builtin_amdgcn_sched_barrier(0);
       // The softmax of block 0 runs in the S/dP slots of block 1 and that of
@@ -552,6 +554,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
         constexpr int m = decltype(mc)::value;
         mfma_slot(m);
         if constexpr (m + LA < NSLOT) read_op(m + LA);
+        if constexpr (m == NSD - 3) init_block(1);
         if constexpr (m >= NSD && m < 2 * NSD) {
           static_for<0, EPS0>([&](auto ec) {
             constexpr int r = (m - NSD) * EPS0 + decltype(ec)::value;
