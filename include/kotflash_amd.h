@@ -111,8 +111,8 @@ int kf_attn_bwd_stages(int stages, const void* q, const void* k, const void* v, 
 /*
  * Number of KV splits the gfx950 decode planner picks for a short-query,
  * long-cache problem: about one workgroup per CU, each split a whole number of
- * key stages (256 keys for D <= 64, 128 above). kf_attn_decode accepts any
- * count whose rounded chunk partitions Sk into exactly that many splits.
+ * 128-key granules. kf_attn_decode accepts any count whose chunk (rounded up
+ * to whole granules) partitions Sk into exactly that many splits.
  */
 int kf_decode_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D);
 

@@ -6,14 +6,15 @@
 //    those rows for one (batch, kv_head) and one KV chunk, so every K/V byte of
 //    the chunk is read from HBM once for all rows of the group (the reference
 //    re-reads K/V once per query head, triton_decode.py:16-104).
-//  * The chunk is streamed in stages of NKEY keys (all of a stage's loads are
-//    issued together, and the next stage's loads are in flight while the
-//    current one is computed); the 4 waves each take NKEY / 4 keys of a stage
-//    and all rows, keeping their own online-softmax state (S^T = K Q^T per 32
-//    keys, P^T feeding O^T += V^T P^T as in the forward).
-//  * At the end the 4 per-wave states are merged in LDS in a fixed order
-//    (deterministic), and the workgroup writes either the final O/LSE (one
-//    split) or an fp32 partial (O_s, LSE_s) of its row block.
+//  * The chunk is cut into 32-key steps that the 4 waves take in turn (so
+//    chunks are whole 128-key granules). Each wave streams its own steps with
+//    no workgroup barrier: its K and V tiles go into a wave-private LDS ring
+//    by direct-to-LDS loads (two steps in flight), and the wave keeps its own
+//    online-softmax state
+//    (S^T = K Q^T per step, P^T feeding O^T += V^T P^T as in the forward).
+//  * At the end the 4 per-wave states are merged in LDS in one pass with a
+//    fixed order (deterministic), and the workgroup writes either the final
+//    O/LSE (one split) or an fp32 partial (O_s, LSE_s) of its row block.
 //  * Keys at or beyond the per-batch visible length L_b are masked; a split
 //    with no visible key writes O_s = 0, LSE_s = -inf (weight 0 in the merge),
 //    as the reference does (triton_forward.py:240-246).
@@ -53,28 +54,27 @@ struct DecParams {
   float scale_log2;
 };
 
-// Keys per stage: 256 for head dims up to 64 (64 KiB of K/V per stage), 128
-// above (the stage buffers then take 72 KiB of LDS).
-template <int DT> struct DecodeStage { static constexpr int NKEY = DT <= 64 ? 256 : 128; };
+// Keys per split granule: the four waves of a workgroup take 32-key steps in
+// turn, so chunks are whole multiples of 128 keys.
+constexpr int kDecGranule = 128;
 
 template <typename T, int DT, int QB>
 __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
-  constexpr int NKEY = DecodeStage<DT>::NKEY;
-  constexpr int KPW = NKEY / 4;  // keys per wave and stage
-  constexpr int KSTR = DT + 8;
-  constexpr int VSTR = DT + 16;
-  constexpr int KT = NKEY * KSTR;
-  constexpr int STAGE = KT + NKEY * VSTR;
   constexpr int CPR = DT / 8;
-  constexpr int CPT = NKEY * CPR / 256;
   constexpr int NKS = DT / 16;
   constexpr int NDB = DT / 32;
-  constexpr int RB = 32 * QB;  // rows per workgroup
-  constexpr int OSTR = DT + 1;
-  // Stage buffer, reused at the end for the cross-wave merge.
-  constexpr int MERGE_BYTES = (4 * RB + 2 * RB + 2 * RB * OSTR) * 4;
-  constexpr int SMEM_ELEMS = (STAGE * 2 > MERGE_BYTES ? STAGE * 2 : MERGE_BYTES) / 2;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM_ELEMS];
+  constexpr int RB = 32 * QB;          // rows per workgroup
+  constexpr int RING = 2;              // 32-key steps in flight per wave
+  constexpr int VT = 32 * DT;          // elements of one K (or V) step tile
+  constexpr int NVI = 32 * CPR / 64;   // 1 KB DMA instructions per step tile
+  constexpr int NL = 2 * NVI;          // memory instructions per step (K and V)
+  constexpr int OSTR = DT + 1;         // padded rows of the merge buffer
+  using Tile = SwizzledTile<CPR>;
+  static_assert(32 * CPR % 64 == 0, "V step tiles must split into whole DMA instructions");
+  // Per wave: RING (K, V) step tiles; reused at the end for the cross-wave merge.
+  constexpr int VBYTES = 4 * RING * 2 * VT * 2;
+  constexpr int MBYTES = (4 * RB * OSTR + 8 * RB) * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[VBYTES > MBYTES ? VBYTES : MBYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
@@ -92,25 +92,12 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   const int L = p.seqlens ? min(max(p.seqlens[b], 0), p.Sk) : p.Sk;
   const int c0 = split * p.chunk;
   const int c1 = min(c0 + p.chunk, L);
-  const int nst = c1 > c0 ? cdiv(c1 - c0, NKEY) : 0;
+  // This wave's steps: 32-key blocks c0 + 32 (wave + 4 j), j = 0 .. nst - 1.
+  const int nst = c1 > c0 + 32 * wave ? cdiv(c1 - c0 - 32 * wave, 128) : 0;
 
   const auto kr = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, rows_extent(p.Sk, p.k_ss, p.D));
   const auto vr = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, rows_extent(p.Sk, p.v_ss, p.D));
-
-  u32x4 kreg[CPT], vreg[CPT];
-  auto gload = [&](int st) {
-    const int kbase = c0 + st * NKEY;
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int e = tid + 256 * c;
-      const int row = e / CPR, col = e % CPR;
-      const int key = kbase + row;
-      const bool ok = key < c1 && col * 8 < p.D;
-      kreg[c] = buf_load16(kr, ok ? (uint32_t)(key * p.k_ss + col * 8) * 2u : kOOB);
-      vreg[c] = buf_load16(vr, ok ? (uint32_t)(key * p.v_ss + col * 8) * 2u : kOOB);
-    }
-  };
-  if (nst > 0) gload(0);
+  uint16_t* kvring = reinterpret_cast<uint16_t*>(smem) + wave * RING * 2 * VT;  // [slot][K | V]
 
   // Q rows as MFMA B operands (lane = packed row).
   u32x4 qf[QB][NKS];
@@ -127,6 +114,34 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
       qf[qb][ks] = buf_load16(qr, (ok && d < p.D) ? (uint32_t)(g * p.q_sh + i * p.q_ss + d) * 2u : kOOB);
     }
   }
+  const float sl2 = fabsf(p.scale_log2);
+  // Per-lane DMA plan: the tile row this lane fills in each instruction
+  // (huge for head-dim padding) and its chunk's byte offset in the row.
+  int vrow[NVI];
+  uint32_t vcol[NVI];
+#pragma unroll
+  for (int k = 0; k < NVI; ++k) {
+    const int pc = k * 64 + lane;
+    const int r = pc / CPR;
+    const int c = (pc % CPR) ^ (r & (Tile::SW - 1));
+    vrow[k] = c * 8 < p.D ? r : 0x7fffffff;
+    vcol[k] = (uint32_t)c * 16u;
+  }
+  // Step j of this wave: its K and V tiles (32 keys) into the wave's LDS
+  // ring by direct-to-LDS loads. Every load of the loop is of this kind, so
+  // the compiler tracks none of them and the explicit waits below are the
+  // only ones (a compiler wait on a register load would drain the ring).
+  auto issue = [&](int j, auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;
+    const int kb0 = c0 + 32 * (wave + 4 * j);
+#pragma unroll
+    for (int k = 0; k < NVI; ++k) {
+      const bool ok = vrow[k] < c1 - kb0;
+      const uint32_t row = (uint32_t)(kb0 + vrow[k]);
+      dma16(kr, kvring + slot * 2 * VT + k * 512, ok ? row * (uint32_t)(p.k_ss * 2) + vcol[k] : kOOB);
+      dma16(vr, kvring + slot * 2 * VT + VT + k * 512, ok ? row * (uint32_t)(p.v_ss * 2) + vcol[k] : kOOB);
+    }
+  };
 
   f32x16 oacc[QB][NDB];
   float m_i[QB], l_i[QB];
@@ -137,128 +152,132 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db) oacc[qb][db] = zero16();
   }
-  wait_all_memory();
 
-  for (int st = 0; st < nst; ++st) {
-    {
-      uint16_t* Ks = smem;
-      uint16_t* Vs = smem + KT;
+  // One 32-key step from ring slot `slot`.
+  auto step = [&](int j, auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;
+    const int kb0 = c0 + 32 * (wave + 4 * j);
+    const uint16_t* Ks = kvring + slot * 2 * VT;
+    const uint16_t* Vs = Ks + VT;
+    u32x4 ka[NKS];  // K rows as MFMA A operands: lane = key, slots = head_dim
 #pragma unroll
-      for (int c = 0; c < CPT; ++c) {
-        const int e = tid + 256 * c;
-        const int row = e / CPR, col = e % CPR;
-        lds_write16(Ks + row * KSTR + col * 8, kreg[c]);
-        lds_write16(Vs + row * VSTR + col * 8, vreg[c]);
-      }
+    for (int ks = 0; ks < NKS; ++ks) ka[ks] = lds_read16(Ks + Tile::chunk(l32, 2 * ks + h32) * 8);
+    f32x16 s[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      s[qb] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) s[qb] = Elem<T>::mfma(ka[ks], qf[qb][ks], s[qb]);
     }
-    __syncthreads();
-    if (st + 1 < nst) gload(st + 1);
+    // S^T layout: lane = row, register r = key kb0 + 8 (r/4) + 4 h + r % 4.
+    const int lim = c1 - kb0;  // keys c < lim are visible
+    u32x4 pk[QB][2];
 #pragma unroll
-    for (int kb = 0; kb < KPW / 32; ++kb) {
-      const int kbase = c0 + st * NKEY + wave * KPW + kb * 32;
-      if (kbase < c1) {
-        const uint16_t* Ks = smem + (wave * KPW + kb * 32) * KSTR;
-        const uint16_t* Vs = smem + KT + (wave * KPW + kb * 32) * VSTR;
-        f32x16 s[QB];
+    for (int qb = 0; qb < QB; ++qb) {
+      if (lim < 32) {
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) s[qb] = zero16();
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const u32x4 a = lds_read16(Ks + l32 * KSTR + 16 * ks + 8 * h32);
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) s[qb] = Elem<T>::mfma(a, qf[qb][ks], s[qb]);
+        for (int r = 0; r < 16; ++r) {
+          const int c = 8 * (r >> 2) + 4 * h32 + (r & 3);
+          s[qb][r] = c < lim ? s[qb][r] : kNegInf;
         }
-        const bool need_mask = kbase + 32 > c1;
-        u32x4 pk[QB][2];
+      }
+      float mx = kNegInf;
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          float mx = kNegInf;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float x = s[qb][r] * p.scale_log2;
-            if (need_mask) {
-              const int key = kbase + 8 * (r >> 2) + 4 * h32 + (r & 3);
-              x = key >= c1 ? kNegInf : x;
-            }
-            s[qb][r] = x;
-            mx = fmaxf(mx, x);
-          }
-          mx = wave_xor32_max(mx);
-          const float m_new = fmaxf(m_i[qb], mx);
-          const float msub = (m_new == kNegInf) ? 0.f : m_new;
-          const float alpha = fast_exp2(m_i[qb] - msub);
-          float rs = 0.f;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float e = fast_exp2(s[qb][r] - msub);
-            s[qb][r] = e;
-            rs += e;
-          }
-          l_i[qb] = l_i[qb] * alpha + rs;
-          m_i[qb] = m_new;
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][r]);
+      mx = wave_xor32_max(mx) * sl2;
+      if (m_i[qb] == kNegInf) {
+        m_i[qb] = mx;
+      } else {
+        const bool grow = mx > m_i[qb] + kRescaleThreshold;
+        if (wave_any(grow)) {
+          const float alpha = grow ? fast_exp2(m_i[qb] - mx) : 1.f;
+          l_i[qb] *= alpha;
 #pragma unroll
           for (int db = 0; db < NDB; ++db) oacc[qb][db] *= alpha;
-          pk[qb][0] = pack8<T>(s[qb], 0);
-          pk[qb][1] = pack8<T>(s[qb], 8);
-        }
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-          for (int stp = 0; stp < 2; ++stp) {
-            const u32x4 a = lds_read_tr_operand(Vs, VSTR, 16 * stp, 32 * db, lane);
-#pragma unroll
-            for (int qb = 0; qb < QB; ++qb) oacc[qb][db] = Elem<T>::mfma(a, pk[qb][stp], oacc[qb][db]);
-          }
+          m_i[qb] = grow ? mx : m_i[qb];
         }
       }
-    }
-    __syncthreads();
-  }
-
-  // Cross-wave merge: M = max_w m_w, O = sum_w 2^(m_w - M) O_w, l likewise.
-  // Waves 0/1 write their rescaled state into LDS slots 0/1, then waves 2/3
-  // add theirs (fixed order: deterministic). Slot rows are padded by one float
-  // so the 32 lanes writing one column of 32 rows hit 32 different banks.
-  float* mbuf = reinterpret_cast<float*>(smem);  // [4][RB] per-wave row max
-  float* lbuf = mbuf + 4 * RB;                   // [2][RB]
-  float* obuf = lbuf + 2 * RB;                   // [2][RB][OSTR]
+      const float msub = (m_i[qb] == kNegInf) ? 0.f : m_i[qb];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    l_i[qb] = wave_xor32_sum(l_i[qb]);
-    if (h32 == 0) mbuf[wave * RB + qb * 32 + l32] = m_i[qb];
+      for (int r = 0; r < 16; ++r) s[qb][r] = fast_exp2(fmaf(s[qb][r], sl2, -msub));
+      pk[qb][0] = pack8<T>(s[qb], 0);
+      pk[qb][1] = pack8<T>(s[qb], 8);
+      // The denominator sums the rounded P that the PV product consumes.
+      float rs0 = 0.f, rs1 = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < 2; ++w2) {
+        rs0 = sum2_acc<T>(pk[qb][w2][0], rs0);
+        rs1 = sum2_acc<T>(pk[qb][w2][1], rs1);
+        rs0 = sum2_acc<T>(pk[qb][w2][2], rs0);
+        rs1 = sum2_acc<T>(pk[qb][w2][3], rs1);
+      }
+      l_i[qb] += rs0 + rs1;
+    }
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+      for (int stp = 0; stp < 2; ++stp) {
+        const u32x4 a = lds_read_tr_operand_sw<CPR>(Vs, 16 * stp, 32 * db, lane);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) oacc[qb][db] = Elem<T>::mfma(a, pk[qb][stp], oacc[qb][db]);
+      }
+    }
+  };
+
+  // Ring: steps j .. j + RING - 1 are in flight; before step j the wave waits
+  // for its loads (those of later steps may remain outstanding), and after it
+  // refills the slot with step j + RING. A wave only ever reads its own LDS
+  // slots, so no workgroup barrier is needed until the merge.
+  static_for<0, RING>([&](auto sc) {
+    if (decltype(sc)::value < nst) issue(decltype(sc)::value, sc);
+  });
+  // Q (issued first) is needed from the first step on; waiting for it only
+  // now overlaps its latency with that of the ring's first loads.
+  wait_all_memory();
+  // Scores are reduced before scaling, which needs a positive scale: for a
+  // negative one Q is negated (exact) and |scale| (sl2) used.
+  if (p.scale_log2 < 0.f) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) qf[qb][ks] ^= 0x80008000u;
   }
-  __syncthreads();
-  float cw[QB];
+  for (int j0 = 0; j0 < nst; j0 += RING) {
+    static_for<0, RING>([&](auto sc) {
+      constexpr int slot = decltype(sc)::value;
+      const int j = j0 + slot;
+      if (j < nst) {
+        const int later = min(RING - 1, nst - 1 - j);  // steps issued after j
+        if (later >= 1) KF_WAIT_VMCNT(NL);
+        else KF_WAIT_VMCNT(0);
+        step(j, sc);
+        if (j + RING < nst) issue(j + RING, sc);
+      }
+    });
+  }
+  static_assert(RING == 2, "the waits above assume at most one later step in flight");
+
+  // Cross-wave merge in one pass: every wave stores (m, l, O) of its rows;
+  // then each output element combines the four waves in a fixed order.
+  __syncthreads();  // all waves are done with their V rings
+  float* obuf = reinterpret_cast<float*>(smem);  // [4][RB][OSTR]
+  float* mbuf = obuf + 4 * RB * OSTR;            // [4][RB]
+  float* lbuf = mbuf + 4 * RB;                   // [4][RB]
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int r = qb * 32 + l32;
-    const float M = fmaxf(fmaxf(mbuf[r], mbuf[RB + r]), fmaxf(mbuf[2 * RB + r], mbuf[3 * RB + r]));
-    cw[qb] = (M == kNegInf) ? 0.f : fast_exp2(m_i[qb] - M);
-  }
-  for (int round = 0; round < 2; ++round) {
-    if ((wave >> 1) == round) {
-      const int slot = wave & 1;
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        const int r = qb * 32 + l32;
-        float* orow = obuf + (slot * RB + r) * OSTR;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-          for (int rr = 0; rr < 16; ++rr) {
-            const int d = 32 * db + 8 * (rr >> 2) + 4 * h32 + (rr & 3);
-            const float val = cw[qb] * oacc[qb][db][rr];
-            orow[d] = round == 0 ? val : orow[d] + val;
-          }
-        }
-        if (h32 == 0) {
-          float* lp = lbuf + slot * RB + r;
-          *lp = round == 0 ? cw[qb] * l_i[qb] : *lp + cw[qb] * l_i[qb];
-        }
-      }
+    const float lt = wave_xor32_sum(l_i[qb]);
+    if (h32 == 0) {
+      mbuf[wave * RB + r] = m_i[qb];
+      lbuf[wave * RB + r] = lt;
     }
-    __syncthreads();
+    float* orow = obuf + (wave * RB + r) * OSTR;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) orow[32 * db + 8 * (rr >> 2) + 4 * h32 + (rr & 3)] = oacc[qb][db][rr];
   }
+  __syncthreads();
 
   // Output: final O/LSE (one split) or this split's fp32 partial.
   const int nrow = min(RB, R - rb * RB);
@@ -267,22 +286,30 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   const int64_t pbase = ((int64_t)grp * p.nsplit + split) * RB;
   for (int e = tid; e < nrow * DQ; e += 256) {
     const int r = e / DQ, d = (e % DQ) * 4;
-    const float M = fmaxf(fmaxf(mbuf[r], mbuf[RB + r]), fmaxf(mbuf[2 * RB + r], mbuf[3 * RB + r]));
-    const float lt = lbuf[r] + lbuf[RB + r];
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, mbuf[w * RB + r]);
+    const float Ms = M == kNegInf ? 0.f : M;
+    float lt = 0.f;
+    float4 ov = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float cw = fast_exp2(mbuf[w * RB + r] - Ms);
+      const float* o = obuf + (w * RB + r) * OSTR + d;
+      lt += cw * lbuf[w * RB + r];
+      ov.x += cw * o[0]; ov.y += cw * o[1]; ov.z += cw * o[2]; ov.w += cw * o[3];
+    }
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    const float* o0 = obuf + r * OSTR + d;
-    const float* o1 = obuf + (RB + r) * OSTR + d;
-    const float4 ov = make_float4((o0[0] + o1[0]) * inv, (o0[1] + o1[1]) * inv,
-                                  (o0[2] + o1[2]) * inv, (o0[3] + o1[3]) * inv);
+    ov.x *= inv; ov.y *= inv; ov.z *= inv; ov.w *= inv;
     const float lse_val = lt > 0.f ? (M + fast_log2(lt)) * kLn2 : kNegInf;
     if (p.nsplit == 1) {
       const int rho = rb * RB + r;
       const int g = rho / p.Sq, i = rho % p.Sq;
       const int h = kvh * p.G + g;
-      u32x2 w;
-      w[0] = pack2<T>(ov.x, ov.y);
-      w[1] = pack2<T>(ov.z, ov.w);
-      *reinterpret_cast<u32x2*>(p.o + b * p.o_sb + h * p.o_sh + i * p.o_ss + d) = w;
+      u32x2 w2;
+      w2[0] = pack2<T>(ov.x, ov.y);
+      w2[1] = pack2<T>(ov.z, ov.w);
+      *reinterpret_cast<u32x2*>(p.o + b * p.o_sb + h * p.o_sh + i * p.o_ss + d) = w2;
       if (d == 0 && p.lse) p.lse[((int64_t)b * p.Hq + h) * p.Sq + i] = lse_val;
     } else {
       *reinterpret_cast<float4*>(p.part_o + (pbase + r) * p.D + d) = ov;
@@ -291,86 +318,97 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   }
 }
 
-// Merge of the split partials: one workgroup per output row.
+// Merge of the split partials: one workgroup per output row. Thread
+// (q = tid % DQ, sl = tid / DQ) owns 4 columns of splits sl, sl + SL, ...; it
+// issues the loads of up to kMergeU of its splits (LSE and O) before using
+// any, so a chunk of kMergeU * SL splits costs one memory round trip: the
+// common case (nsplit <= kMergeU * SL) reads everything in one trip.
+constexpr int kMergeU = 8;
+
 template <typename T>
 __global__ __launch_bounds__(256) void merge_kernel(const DecParams p) {
   const int tid = threadIdx.x;
   const int RB = p.rb_rows;
-  const int r = blockIdx.x % RB;
-  const int grp = blockIdx.x / RB;
-  const int rb = grp % p.nrb;
-  const int bk = grp / p.nrb;
+  const int R = p.G * p.Sq;
+  // blockIdx -> (b, kvh, packed row rho); partial rows are grouped by row block.
+  const int rho_all = blockIdx.x % R;
+  const int bk = blockIdx.x / R;
   const int kvh = bk % p.Hkv, b = bk / p.Hkv;
-  const int rho = rb * RB + r;
-  if (rho >= p.G * p.Sq) return;
-  const int g = rho / p.Sq, i = rho % p.Sq;
+  const int rb = rho_all / RB, r = rho_all % RB;
+  const int grp = (b * p.Hkv + kvh) * p.nrb + rb;
+  const int g = rho_all / p.Sq, i = rho_all % p.Sq;
   const int h = kvh * p.G + g;
   const float* plse = p.part_lse + (int64_t)grp * p.nsplit * RB + r;
   const float* po = p.part_o + (int64_t)grp * p.nsplit * RB * p.D + (int64_t)r * p.D;
   __shared__ float red[8];
   __shared__ float4 acc4[256];
 
-  // Max and weight sum of the split LSEs (block reduction).
-  float mx = kNegInf;
-  for (int sp = tid; sp < p.nsplit; sp += 256) mx = fmaxf(mx, plse[(int64_t)sp * RB]);
+  const int DQ = p.D / 4;
+  const int SL = 256 / DQ;
+  const int q = tid % DQ, sl = tid / DQ;
+  const bool active = sl < SL;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float den = 0.f, mrun = kNegInf;  // running reference max of this thread's chunks
+  for (int c0 = 0; c0 < p.nsplit; c0 += kMergeU * SL) {
+    float4 v[kMergeU];
+    float w[kMergeU];
+#pragma unroll
+    for (int u = 0; u < kMergeU; ++u) {
+      const int s2 = c0 + sl + SL * u;
+      const bool ok = active && s2 < p.nsplit;
+      v[u] = ok ? *reinterpret_cast<const float4*>(po + (int64_t)s2 * RB * p.D + 4 * q)
+                : make_float4(0.f, 0.f, 0.f, 0.f);
+      w[u] = ok ? plse[(int64_t)s2 * RB] * kLog2e : kNegInf;
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int u = 0; u < kMergeU; ++u) mx = fmaxf(mx, w[u]);
+    // Thread-local online rescale across chunks (one chunk in the common case).
+    const float mnew = fmaxf(mrun, mx);
+    const float ms = mnew == kNegInf ? 0.f : mnew;
+    const float alpha = fast_exp2(mrun - ms);
+    acc.x *= alpha; acc.y *= alpha; acc.z *= alpha; acc.w *= alpha;
+    den *= alpha;
+#pragma unroll
+    for (int u = 0; u < kMergeU; ++u) {
+      const float wt = fast_exp2(w[u] - ms);
+      den += wt;
+      acc.x += wt * v[u].x; acc.y += wt * v[u].y; acc.z += wt * v[u].z; acc.w += wt * v[u].w;
+    }
+    mrun = mnew;
+  }
+  // Block-wide max of the per-thread reference maxima, then rescale.
+  float mx = mrun;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float ms = (mx == kNegInf) ? 0.f : mx;
-  float den = 0.f;
-  for (int sp = tid; sp < p.nsplit; sp += 256)
-    den += fast_exp2((plse[(int64_t)sp * RB] - ms) * kLog2e);
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float Ms = M == kNegInf ? 0.f : M;
+  const float sc = fast_exp2(mrun - Ms);
+  acc.x *= sc; acc.y *= sc; acc.z *= sc; acc.w *= sc;
+  den *= sc;
+  // Every split's weight was counted once per column group; use q == 0's.
+  float dsum = q == 0 ? den : 0.f;
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off);
-  if ((tid & 63) == 0) red[4 + (tid >> 6)] = den;
+  for (int off = 32; off > 0; off >>= 1) dsum += __shfl_xor(dsum, off);
   __syncthreads();
-  den = red[4] + red[5] + red[6] + red[7];
-
-  // Weighted sum: thread -> (4-column group q, split lane sl); all of a
-  // thread's loads are issued before they are consumed.
-  const int DQ = p.D / 4;
-  const int SL = 256 / DQ;
-  const int q = tid % DQ, sl = tid / DQ;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (sl < SL) {
-    constexpr int UNR = 4;
-    for (int sp = sl; sp < p.nsplit; sp += SL * UNR) {
-      float4 v[UNR];
-      float w[UNR];
-#pragma unroll
-      for (int u = 0; u < UNR; ++u) {
-        const int s2 = sp + SL * u;
-        const bool ok = s2 < p.nsplit;
-        v[u] = ok ? *reinterpret_cast<const float4*>(po + (int64_t)s2 * RB * p.D + 4 * q)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
-        w[u] = ok ? plse[(int64_t)s2 * RB] : kNegInf;
-      }
-#pragma unroll
-      for (int u = 0; u < UNR; ++u) {
-        const float wt = fast_exp2((w[u] - ms) * kLog2e);
-        acc.x += wt * v[u].x;
-        acc.y += wt * v[u].y;
-        acc.z += wt * v[u].z;
-        acc.w += wt * v[u].w;
-      }
-    }
-  }
+  if ((tid & 63) == 0) red[4 + (tid >> 6)] = dsum;
   acc4[tid] = acc;
   __syncthreads();
+  const float dtot = red[4] + red[5] + red[6] + red[7];
   if (tid < DQ) {
     for (int s2 = 1; s2 < SL; ++s2) {
       const float4 o2 = acc4[s2 * DQ + tid];
       acc.x += o2.x; acc.y += o2.y; acc.z += o2.z; acc.w += o2.w;
     }
-    const float inv = den > 0.f ? 1.f / den : 0.f;
+    const float inv = dtot > 0.f ? 1.f / dtot : 0.f;
     u32x2 wv;
     wv[0] = pack2<T>(acc.x * inv, acc.y * inv);
     wv[1] = pack2<T>(acc.z * inv, acc.w * inv);
     *reinterpret_cast<u32x2*>(p.o + b * p.o_sb + h * p.o_sh + i * p.o_ss + 4 * tid) = wv;
     if (tid == 0 && p.lse)
-      p.lse[((int64_t)b * p.Hq + h) * p.Sq + i] = den > 0.f ? mx + fast_log2(den) * kLn2 : kNegInf;
+      p.lse[((int64_t)b * p.Hq + h) * p.Sq + i] = dtot > 0.f ? (M + fast_log2(dtot)) * kLn2 : kNegInf;
   }
 }
 
@@ -390,7 +428,7 @@ static int launch_decode(DecParams p, hipStream_t stream) {
     hipLaunchKernelGGL((decode_kernel<T, DT, 1>), dim3((unsigned)grid), dim3(256), 0, stream, p);
   int rc = check_launch("kf_attn_decode(split)");
   if (rc || p.nsplit == 1) return rc;
-  const int64_t mgrid = (int64_t)p.B * p.Hkv * p.nrb * p.rb_rows;
+  const int64_t mgrid = (int64_t)p.B * p.Hkv * R;
   hipLaunchKernelGGL((merge_kernel<T>), dim3((unsigned)mgrid), dim3(256), 0, stream, p);
   return check_launch("kf_attn_decode(merge)");
 }
@@ -416,8 +454,8 @@ extern "C" int kf_decode_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t 
   const int64_t nrb = (G * Sq + decode_rows_per_wg(G, Sq) - 1) / decode_rows_per_wg(G, Sq);
   const int64_t units = B * Hkv * nrb;
   // About one workgroup per CU (256 CUs, two resident each), each streaming
-  // whole stages; splits only add merge traffic beyond that.
-  const int64_t stage = D <= 64 ? 256 : 128;
+  // whole 128-key granules; splits only add merge traffic beyond that.
+  const int64_t stage = kDecGranule;
   const int64_t target = 256;
   int64_t ns = (target + units - 1) / units;
   const int64_t max_ns = (Sk + stage - 1) / stage;
@@ -457,7 +495,7 @@ extern "C" int kf_attn_decode(const void* q, const void* k, const void* v, void*
     return rc;
   if (!(scale == scale) || scale - scale != 0.f) return set_error(KF_EINVAL, "%s: scale must be finite", what);
   if (num_splits < 1) return set_error(KF_EINVAL, "%s: num_splits must be >= 1", what);
-  const int64_t stage = D <= 64 ? 256 : 128;
+  const int64_t stage = kDecGranule;
   const int64_t chunk = ((Sk + num_splits - 1) / num_splits + stage - 1) / stage * stage;
   if ((Sk + chunk - 1) / chunk != num_splits)
     return set_error(KF_EINVAL, "%s: num_splits=%d does not partition Sk=%lld into whole %lld-key "

@@ -88,7 +88,7 @@ def test_decode_planner_and_workspace():
     lib = _hip.lib()
     for sk in (2048, 4096, 8192, 16384, 1537, 8193, 100000):
         ns = lib.kf_decode_num_splits(2, 8, 2, 1, sk, 64)
-        chunk = ((-(-sk // ns)) + 255) // 256 * 256
+        chunk = ((-(-sk // ns)) + 127) // 128 * 128  # whole 128-key granules
         assert ns >= 1 and -(-sk // chunk) == ns
     assert lib.kf_decode_num_splits(2, 8, 2, 1, 16384, 64) == 64
     assert lib.kf_decode_workspace_bytes(2, 8, 2, 1, 64, 1) == 0
