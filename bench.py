@@ -5,7 +5,8 @@ One JSON line on stdout (everything else goes to stderr):
 
 * ``value``: causal GQA fwd+bwd TFLOP/s at BASELINE config 3 (B=2, Hq=16,
   Hkv=4, S=4096, D=128, fp16, q/k/v ~ 0.5 N(0,1), dO ~ N(0,1)). A step is one
-  forward plus one backward (4 launches: forward, row delta, dQ, dK/dV) on
+  forward plus one backward (4 launches: forward, dQ with the row deltas,
+  dK/dV, dK/dV fixup) on
   inputs already resident in HBM; exactly ``--steps`` steps are timed between
   two ``torch.cuda.synchronize()``. Work per step is the algorithmic
   4.8115e11 FLOP (forward 4 D B Hq S(S+1)/2, backward 2.5x that).
@@ -86,7 +87,7 @@ def bench_train(torch, _hip, dtype, steps, warmup):
 
     def step(ev=None):
         fwd()
-        bwd(_hip.KF_BWD_DELTA | _hip.KF_BWD_DQ)
+        bwd(_hip.KF_BWD_DELTA | _hip.KF_BWD_DQ)  # dQ kernel (computes the row deltas too)
         if ev is not None:
             ev[0].record()
         bwd(_hip.KF_BWD_DKDV)
@@ -130,14 +131,12 @@ def bench_train(torch, _hip, dtype, steps, warmup):
 
     per = {
         "attn_fwd": isolated(fwd),
-        "bwd_delta": isolated(lambda: bwd(_hip.KF_BWD_DELTA)),
         "bwd_dq": isolated(lambda: bwd(_hip.KF_BWD_DQ)),
         "bwd_dkdv": isolated(lambda: bwd(_hip.KF_BWD_DKDV)),
         "bwd_dkdv_fixup": isolated(lambda: bwd(_hip.KF_BWD_DKDV_FIXUP)),
     }
     f = fwd_flops(b, hq, s, d)
-    work = {"attn_fwd": f, "bwd_delta": 0.0, "bwd_dq": 0.5 * f, "bwd_dkdv": 2.0 * f,
-            "bwd_dkdv_fixup": 0.0}
+    work = {"attn_fwd": f, "bwd_dq": 0.5 * f, "bwd_dkdv": 2.0 * f, "bwd_dkdv_fixup": 0.0}
     return ms, wall_ms, dkdv_live, per, work, 3.5 * f
 
 

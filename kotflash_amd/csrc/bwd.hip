@@ -5,6 +5,8 @@
 //      low-precision O (reference triton_backward.py:45), stored negated,
 //      and LSE[i] log2(e), for the dK/dV kernel, which loads both rows
 //      straight into LDS and starts its dP accumulators at -delta.
+//      (When dq_kernel runs it computes both itself, and the separate launch
+//      is skipped.)
 //   2. dq_kernel (query-stationary, same layout as the forward, two waves per
 //      SIMD): per key tile it recomputes S^T = K Q^T and dP^T = V dO^T, forms
 //      dS^T = P^T (dP^T - delta) with P = exp(scale S - LSE), and accumulates
@@ -177,7 +179,33 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
   }
   const int64_t rowlin = ((int64_t)b * p.Hq + h) * p.Sq + qrow;
   const float lse2 = row_ok ? p.lse[rowlin] * kLog2e : 0.f;
-  const float dlt = row_ok ? -p.delta[rowlin] : 0.f;  // the workspace holds -delta
+  // Row delta = rowsum(O * dO) from the stored O (reference
+  // triton_backward.py:45): this lane holds 8 head_dim slots per k-step of
+  // its row for dO; the same slots of O give the lane's share, and the other
+  // half of the row is in lane ^ 32. The dK/dV kernel reads -delta and
+  // LSE * log2(e) from the workspace, written here by one lane per row.
+  float dlt = 0.f;
+  {
+    const auto orr = make_rsrc(p.o + b * p.o_sb + h * p.o_sh, rows_extent(p.Sq, p.o_ss, p.D));
+    u32x4 of[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d = 16 * ks + 8 * h32;
+      of[ks] = buf_load16(orr, row_ok && d < p.D ? (uint32_t)(qrow * p.o_ss + d) * 2u : kOOB);
+    }
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        dlt += Elem<T>::to_f32((uint16_t)(of[ks][w] & 0xffff)) * Elem<T>::to_f32((uint16_t)(dof[ks][w] & 0xffff));
+        dlt += Elem<T>::to_f32((uint16_t)(of[ks][w] >> 16)) * Elem<T>::to_f32((uint16_t)(dof[ks][w] >> 16));
+      }
+    dlt = wave_xor32_sum(dlt);
+    if (row_ok && h32 == 0) {
+      p.delta[rowlin] = -dlt;
+      p.lse2[rowlin] = lse2;
+    }
+  }
 
   f32x16 dq[NDB];
 #pragma unroll
@@ -720,7 +748,9 @@ static size_t partial_bytes(int nwg, int64_t D) {
 
 template <typename T, int DT>
 static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) {
-  if (stages & KF_BWD_DELTA) {
+  // dq_kernel computes the row deltas itself: the delta launch is only needed
+  // when the dK/dV stage runs without it.
+  if ((stages & KF_BWD_DELTA) && !(stages & KF_BWD_DQ)) {
     const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
     hipLaunchKernelGGL((delta_kernel<T>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, stream, p);
     int rc = check_launch("kf_attn_bwd(delta)");
