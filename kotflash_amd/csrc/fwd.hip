@@ -191,21 +191,36 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
     // masked for it.
     const bool active = !CAUSAL || kbase <= wq0 + QB * 32 - 1;
     if (active) {
+      // S^T = K Q^T as a stream of 2 NKS MFMA slots (key block kb = m / NKS,
+      // k-step ks = m % NKS); each slot also issues the LDS read of the
+      // operand LA slots ahead, the last ones reading the first V^T operands
+      // of the PV product. Fences pin the order: without them the reads are
+      // issued one slot ahead and every MFMA waits for its operand.
+      constexpr int NS = 2 * NKS;   // S slots
+      constexpr int NPV = 4 * NDB;  // PV slots (db = j / 4, key step st = j % 4)
+      constexpr int LA = 4;
+      u32x4 kop[NS], vop[NPV];
+      auto read_k = [&](int m) {
+        kop[m] = lds_read16(Ks + ((m / NKS) * 32 + l32) * KSTR + 16 * (m % NKS) + 8 * h32);
+      };
+      auto read_v = [&](int j) { vop[j] = lds_read_tr_operand(Vs, VSTR, 16 * (j % 4), 32 * (j / 4), lane); };
       f32x16 s[QB][2];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
         s[qb][0] = zero16();
         s[qb][1] = zero16();
       }
+      static_for<0, LA>([&](auto mc) { read_k(decltype(mc)::value); });
+      __builtin_amdgcn_sched_barrier(0);
+      static_for<0, NS>([&](auto mc) {
+        constexpr int m = decltype(mc)::value;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          const u32x4 a = lds_read16(Ks + (kb * 32 + l32) * KSTR + 16 * ks + 8 * h32);
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) s[qb][kb] = Elem<T>::mfma(a, qf[qb][ks], s[qb][kb]);
-        }
-      }
+        for (int qb = 0; qb < QB; ++qb)
+          s[qb][m / NKS] = Elem<T>::mfma(kop[m], qf[qb][m % NKS], s[qb][m / NKS]);
+        if constexpr (m + LA < NS) read_k(m + LA);
+        else if constexpr (m + LA - NS < NPV) read_v(m + LA - NS);
+        __builtin_amdgcn_sched_barrier(0);
+      });
 
       const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && kbase + BN - 1 > wq0);
       u32x4 pk[QB][4];
@@ -267,15 +282,15 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
         l_i[qb] += rs0 + rs1;
       }
 
+      __builtin_amdgcn_sched_barrier(0);
+      static_for<0, NPV>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          const u32x4 a = lds_read_tr_operand(Vs, VSTR, 16 * st, 32 * db, lane);
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) oacc[qb][db] = Elem<T>::mfma(a, pk[qb][st], oacc[qb][db]);
-        }
-      }
+        for (int qb = 0; qb < QB; ++qb)
+          oacc[qb][j / 4] = Elem<T>::mfma(vop[j], pk[qb][j % 4], oacc[qb][j / 4]);
+        if constexpr (j + LA < NPV) read_v(j + LA);
+        __builtin_amdgcn_sched_barrier(0);
+      });
     }
     if (it + 1 < ntiles) sstore(buf ^ 1);
     __syncthreads();
