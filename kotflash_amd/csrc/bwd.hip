@@ -127,8 +127,11 @@ template <typename T, int DT, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
   constexpr int BM = 128;
   constexpr int BN = 64;
-  constexpr int KSTR = DT + 16;  // K: b128 reads for S^T and transposed reads for dQ^T
-  constexpr int VSTR = DT + 8;   // V: b128 reads for dP^T
+  // K is read both as b128 rows (S^T) and transposed (dQ^T); a 48-byte pad at
+  // 256-byte rows (16 bytes otherwise) keeps b128 reads conflict-free and
+  // transposed reads at two-way. V is read as b128 rows only (dP^T).
+  constexpr int KSTR = DT + (DT == 128 ? 24 : 8);
+  constexpr int VSTR = DT + 8;
   constexpr int KT = BN * KSTR;
   constexpr int STAGE = KT + BN * VSTR;
   constexpr int CPR = DT / 8;
@@ -410,7 +413,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
     for (int k = 0; k < NQI; ++k) {
       const int pc = (wave * NQI + k) * 64 + lane;  // physical chunk this lane fills
       const int r = pc / CPR;
-      const int c = (pc % CPR) ^ (r & (Tile::SW - 1));
+      const int c = (pc % CPR) ^ Tile::key(r);
       dma_row[k] = c * 8 < p.D ? r : 0x7fffffff;
       dma_col[k] = (uint32_t)c * 16u;
     }

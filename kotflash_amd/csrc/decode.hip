@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   for (int k = 0; k < NVI; ++k) {
     const int pc = k * 64 + lane;
     const int r = pc / CPR;
-    const int c = (pc % CPR) ^ (r & (Tile::SW - 1));
+    const int c = (pc % CPR) ^ Tile::key(r);
     vrow[k] = c * 8 < p.D ? r : 0x7fffffff;
     vcol[k] = (uint32_t)c * 16u;
   }

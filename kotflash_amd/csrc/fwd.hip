@@ -78,8 +78,12 @@ template <typename T, int DT, int QB, bool CAUSAL>
 __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdParams p) {
   constexpr int BM = 4 * QB * 32;
   constexpr int BN = 64;
-  constexpr int KSTR = DT + 8;   // 16-byte pad: conflict-free b128 row reads
-  constexpr int VSTR = DT + 16;  // 32-byte pad: conflict-free transposed reads
+  // Row strides (elements). K is read by b128 rows (16 lanes per pass over 64
+  // four-byte banks): any stride of 16 mod 32 bytes is conflict-free. V is read
+  // transposed (32 lanes = 4 rows x 64 bytes per pass): a stride of 64 mod 128
+  // bytes puts the 4 rows on disjoint banks.
+  constexpr int KSTR = DT + 8;
+  constexpr int VSTR = DT + ((64 - 2 * DT) % 128 + 128) % 128 / 2;
   constexpr int KT = BN * KSTR;
   constexpr int STAGE = KT + BN * VSTR;
   constexpr int CPR = DT / 8;           // 16-byte chunks per row

@@ -218,13 +218,27 @@ __device__ inline void dma4(__amdgpu_buffer_rsrc_t r, float* lds_base, uint32_t 
 
 // Row-major 16-bit tile of `rows` x (8 cpr) elements stored without padding,
 // 16-byte chunks XOR-swizzled within each row: logical chunk c of row r lives
-// at physical chunk c ^ (r & (sw - 1)), sw the largest power of two (<= 16)
-// dividing cpr. Consecutive rows read at the same logical column then fall on
-// different banks.
+// at physical chunk c ^ key(r). The LDS serves a b128 read 16 lanes per pass
+// and a ds_read_b64_tr_b16 read 32 lanes per pass over 64 four-byte banks, and
+// the kernels read these tiles both ways:
+//   - b128 rows: 16 lanes read 16 consecutive rows at one logical chunk, so
+//     key(r) must differ across any 16 consecutive rows (mod 16);
+//   - transposed: 32 lanes read 4 consecutive rows (from a multiple of 4) x 4
+//     consecutive chunks (from a multiple of 4), so the keys of those 4 rows
+//     must differ in the bits above the chunk's low two.
+// key(r) = rotate(r mod 16) by two bits meets both at 16 chunks per row
+// (measured: 4 passes per b128 read and 2 per transposed read, the minimum;
+// the plain key r mod 16 costs 8 passes per transposed read). Narrower rows
+// use the largest key that keeps c ^ key inside the row.
 template <int CPR>
 struct SwizzledTile {
   static constexpr int SW = (CPR % 16 == 0) ? 16 : (CPR % 8 == 0) ? 8 : 4;
-  __device__ static inline int chunk(int r, int c) { return r * CPR + (c ^ (r & (SW - 1))); }
+  __device__ static inline int key(int r) {
+    if constexpr (SW == 16) return ((r & 3) << 2) | ((r >> 2) & 3);
+    else if constexpr (SW == 8) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+    else return (r >> 2) & 3;
+  }
+  __device__ static inline int chunk(int r, int c) { return r * CPR + (c ^ key(r)); }
   // Element offset of element col (any in [0, 8 cpr)) of row r.
   __device__ static inline int elem(int r, int col) { return chunk(r, col >> 3) * 8 + (col & 7); }
 };
