@@ -404,19 +404,28 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
     wait_all_memory();
 
     // Per-lane DMA plan, fixed for the segment: for each of this wave's NQI
-    // 1 KB blocks of a tile, the tile row this lane fills (or a huge value
-    // when its chunk is head-dim padding, so the row test below fails) and
-    // the byte offset of its chunk within the row.
-    int dma_row[NQI];
-    uint32_t dma_col[NQI];
+    // 1 KB blocks of a tile, the byte offset of this lane's 16-byte chunk
+    // within the tile's rows (kOOB when the chunk is head-dim padding). A
+    // unit adds its first row's offset as the (scalar) soffset; rows past Sq
+    // then fall beyond the resource extent and load as zeros.
+    uint32_t dma_qoff[NQI], dma_doff[NQI];
 #pragma unroll
     for (int k = 0; k < NQI; ++k) {
       const int pc = (wave * NQI + k) * 64 + lane;  // physical chunk this lane fills
       const int r = pc / CPR;
       const int c = (pc % CPR) ^ Tile::key(r);
-      dma_row[k] = c * 8 < p.D ? r : 0x7fffffff;
-      dma_col[k] = (uint32_t)c * 16u;
+      const bool ok = c * 8 < p.D;
+      dma_qoff[k] = ok ? (uint32_t)(r * p.q_ss + c * 8) * 2u : kOOB;
+      dma_doff[k] = ok ? (uint32_t)(r * p.do_ss + c * 8) * 2u : kOOB;
     }
+    // Statistics rows: wave 0 loads LSE * log2(e), wave 1 -delta; waves 2 and
+    // 3 load zeros into the unused rows.
+    const uint32_t dma_soff = wave < 2 ? (uint32_t)lane * 4u : kOOB;
+    // LDS byte addresses (M0) of stage 0's blocks for this wave.
+    const uint32_t lds_q0 = lds_addr(&stage[0][0][0]) + (uint32_t)(wave * NQI) * 1024u;
+    const uint32_t lds_s0 = lds_addr(&rowstat[0][0][0]) + (uint32_t)wave * (kBMQ * 4u);
+    constexpr uint32_t kStageBytes = 2u * QT * 2u;
+    constexpr uint32_t kStatBytes = 4u * kBMQ * 4u;
     // Units are walked in order (query head g, query tile qt): `Walk`
     // advances one unit without divisions.
     struct Walk {
@@ -437,34 +446,37 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
     constexpr int NDMA = 2 * NQI + 1;  // DMA instructions per unit (the last: LSE or delta rows)
     struct Dma {
       __amdgpu_buffer_rsrc_t qr, dor, sr;
-      int qbase, st;
+      uint32_t qso, dso, sso;  // soffsets: the unit's first row
+      uint32_t lq, ls;         // M0 of this wave's first Q block and of its statistics row
     };
-    // A unit past the segment's end gets an out-of-range row base: its loads
-    // then only deposit zeros into the (free) stage, which keeps the issue
-    // unconditional.
+    // A unit past the segment's end gets empty resources: its loads then only
+    // deposit zeros into the (free) stage, which keeps the issue unconditional.
     auto dma_setup = [&](const Walk& w, int st, bool real) {
       Dma d;
       const int h = kvh * p.G + (real ? w.g : 0);
-      d.qbase = real ? w.qt * kBMQ : (1 << 29);
-      d.st = st;
-      d.qr = make_rsrc(p.q + b * p.q_sb + h * p.q_sh, rows_extent(p.Sq, p.q_ss, p.D));
-      d.dor = make_rsrc(p.dout + b * p.do_sb + h * p.do_sh, rows_extent(p.Sq, p.do_ss, p.D));
+      const int q0 = real ? w.qt * kBMQ : 0;
+      d.qr = make_rsrc(p.q + b * p.q_sb + h * p.q_sh, real ? rows_extent(p.Sq, p.q_ss, p.D) : 0u);
+      d.dor = make_rsrc(p.dout + b * p.do_sb + h * p.do_sh,
+                        real ? rows_extent(p.Sq, p.do_ss, p.D) : 0u);
       const int64_t rb = ((int64_t)b * p.Hq + h) * p.Sq;
-      d.sr = make_rsrc(wave == 0 ? p.lse2 + rb : p.delta + rb, (uint32_t)p.Sq * 4u);
+      d.sr = make_rsrc(wave == 0 ? p.lse2 + rb : p.delta + rb, real ? (uint32_t)p.Sq * 4u : 0u);
+      d.qso = (uint32_t)(q0 * p.q_ss) * 2u;
+      d.dso = (uint32_t)(q0 * p.do_ss) * 2u;
+      d.sso = (uint32_t)q0 * 4u;
+      d.lq = lds_q0 + (uint32_t)st * kStageBytes;
+      d.ls = lds_s0 + (uint32_t)st * kStatBytes;
       return d;
     };
     // DMA instruction j of a unit: Q / dO blocks, then the row statistics.
     auto dma_issue = [&](const Dma& d, int j) {
       if (j < 2 * NQI) {
         const int k = j >> 1;
-        const bool isq = (j & 1) == 0;
-        const bool ok = dma_row[k] < p.Sq - d.qbase;
-        const uint32_t ss = (uint32_t)(isq ? p.q_ss : p.do_ss) * 2u;
-        const uint32_t off = ok ? (uint32_t)(d.qbase + dma_row[k]) * ss + dma_col[k] : kOOB;
-        dma16(isq ? d.qr : d.dor, &stage[d.st][isq ? 0 : 1][(wave * NQI + k) * 512], off);
+        if ((j & 1) == 0)
+          dma16_s(d.qr, d.lq + (uint32_t)k * 1024u, dma_qoff[k], d.qso);
+        else
+          dma16_s(d.dor, d.lq + (uint32_t)(QT * 2) + (uint32_t)k * 1024u, dma_doff[k], d.dso);
       } else {
-        const int qi = d.qbase + lane;
-        dma4(d.sr, &rowstat[d.st][wave][0], wave < 2 && qi < p.Sq ? (uint32_t)qi * 4u : kOOB);
+        dma4_s(d.sr, d.ls, dma_soff, d.sso);
       }
     };
 
@@ -570,6 +582,13 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) dp[qb][r] = d4[qb][r >> 2][r & 3];
       };
+      // The dK/dV accumulators are pinned to accumulation registers at the
+      // top of the unit (an empty asm with "+a" operands): left to itself,
+      // the register allocator parks some of them in VGPRs while the S/dP
+      // accumulators take their place, which costs 96 accumulator copies per
+      // unit.
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) asm volatile("" : "+a"(dk[db]), "+a"(dv[db]));
       init_block(0);
       static_for<0, LA>([&](auto mc) { read_op(decltype(mc)::value); });
       __builtin_amdgcn_sched_barrier(0);

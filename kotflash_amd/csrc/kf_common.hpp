@@ -210,6 +210,35 @@ __device__ inline void dma4(__amdgpu_buffer_rsrc_t r, float* lds_base, uint32_t 
       : "memory", "m0");
 }
 
+// The same loads with the LDS destination given as a wave-uniform LDS byte
+// address (M0) and a wave-uniform byte offset added to every lane's (soffset).
+// Both are plain integers here, so callers that compute them from uniform
+// values keep the whole address computation on the scalar unit. A lane's
+// voffset + soffset must stay below 2^32: with voffset < 2^31 (or kOOB) and
+// soffset < 2^31 it does.
+__device__ inline void dma16_s(__amdgpu_buffer_rsrc_t r, uint32_t lds_m0, uint32_t voff,
+                               uint32_t soff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, %3 offen lds"
+      :
+      : "s"(__builtin_amdgcn_readfirstlane(lds_m0)), "v"(voff), "s"(r),
+        "s"(__builtin_amdgcn_readfirstlane(soff))
+      : "memory", "m0");
+}
+__device__ inline void dma4_s(__amdgpu_buffer_rsrc_t r, uint32_t lds_m0, uint32_t voff,
+                              uint32_t soff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dword %1, %2, %3 offen lds"
+      :
+      : "s"(__builtin_amdgcn_readfirstlane(lds_m0)), "v"(voff), "s"(r),
+        "s"(__builtin_amdgcn_readfirstlane(soff))
+      : "memory", "m0");
+}
+
 // s_waitcnt that waits until at most n vector-memory operations of the wave
 // are outstanding (gfx9 encoding: vmcnt bits [3:0] and [15:14], expcnt and
 // lgkmcnt left at their maxima). n must be a compile-time constant < 64.
