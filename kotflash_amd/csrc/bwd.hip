@@ -122,23 +122,23 @@ __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
 // ---------------------------------------------------------------------------
 // 2. dQ, query-stationary: 4 waves x 32 rows, 64-key tiles, two workgroups
 // per CU. Each 32-key block is finished (S, dP, dS, dQ update) before the next
-// starts so the live registers fit two waves per SIMD.
+// starts so the live registers fit two waves per SIMD. K/V tiles stream into
+// a two-stage LDS ring by direct-to-LDS loads (no register staging), stored
+// unpadded with the swizzle of SwizzledTile so that every LDS read of the
+// tile body is a per-lane base register plus an immediate offset.
 template <typename T, int DT, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
   constexpr int BM = 128;
   constexpr int BN = 64;
-  // K is read both as b128 rows (S^T) and transposed (dQ^T); a 48-byte pad at
-  // 256-byte rows (16 bytes otherwise) keeps b128 reads conflict-free and
-  // transposed reads at two-way. V is read as b128 rows only (dP^T).
-  constexpr int KSTR = DT + (DT == 128 ? 24 : 8);
-  constexpr int VSTR = DT + 8;
-  constexpr int KT = BN * KSTR;
-  constexpr int STAGE = KT + BN * VSTR;
   constexpr int CPR = DT / 8;
-  constexpr int CPT = BN * CPR / 256;
   constexpr int NKS = DT / 16;
   constexpr int NDB = DT / 32;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+  constexpr int TB = BN * DT * 2;       // bytes of one K (or V) tile
+  constexpr int STAGE_B = 2 * TB;       // K | V
+  constexpr int NKI = BN * CPR / 256;   // 1 KB loads per wave per tile and matrix
+  static_assert(BN * CPR == 256 * NKI, "tile chunks must split into whole loads");
+  using Tile = SwizzledTile<CPR>;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE_B / 2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
@@ -217,58 +217,101 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
   const int nkeys = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
   const int ntiles = cdiv(nkeys, BN);
 
-  u32x4 kreg[CPT], vreg[CPT];
-  auto gload = [&](int tile) {
-    const int kbase = tile * BN;
+  // Per-lane load plan: for each of this wave's NKI 1 KB blocks of a tile,
+  // the byte offset of this lane's 16-byte chunk within the tile's rows
+  // (kOOB for head-dim padding). The tile's first key enters as soffset;
+  // keys past Sk fall beyond the resource extent and load as zeros.
+  uint32_t koff[NKI], voff[NKI];
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int e = tid + 256 * c;
-      const int row = e / CPR, col = e % CPR;
-      const int key = kbase + row;
-      const bool ok = key < p.Sk && col * 8 < p.D;
-      kreg[c] = buf_load16(kr, ok ? (uint32_t)(key * p.k_ss + col * 8) * 2u : kOOB);
-      vreg[c] = buf_load16(vr, ok ? (uint32_t)(key * p.v_ss + col * 8) * 2u : kOOB);
-    }
-  };
-  auto sstore = [&](int buf) {
-    uint16_t* Ks = smem + buf * STAGE;
-    uint16_t* Vs = Ks + KT;
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int e = tid + 256 * c;
-      const int row = e / CPR, col = e % CPR;
-      lds_write16(Ks + row * KSTR + col * 8, kreg[c]);
-      lds_write16(Vs + row * VSTR + col * 8, vreg[c]);
-    }
-  };
-
-  if (ntiles > 0) {
-    gload(0);
-    sstore(0);
+  for (int k = 0; k < NKI; ++k) {
+    const int pc = (wave * NKI + k) * 64 + lane;
+    const int r = pc / CPR;
+    const int c = (pc % CPR) ^ Tile::key(r);
+    const bool ok = c * 8 < p.D;
+    koff[k] = ok ? (uint32_t)(r * p.k_ss + c * 8) * 2u : kOOB;
+    voff[k] = ok ? (uint32_t)(r * p.v_ss + c * 8) * 2u : kOOB;
   }
+  const uint32_t lds0 = lds_addr(smem);
+  auto tile_load = [&](int tile, int st) {
+    const uint32_t kso = (uint32_t)(tile * BN * p.k_ss) * 2u;
+    const uint32_t vso = (uint32_t)(tile * BN * p.v_ss) * 2u;
+    const uint32_t m0 = lds0 + (uint32_t)st * STAGE_B + (uint32_t)(wave * NKI) * 1024u;
+#pragma unroll
+    for (int k = 0; k < NKI; ++k) {
+      dma16_s(kr, m0 + k * 1024u, koff[k], kso);
+      dma16_s(vr, m0 + TB + k * 1024u, voff[k], vso);
+    }
+  };
+  // LDS read bases (bytes, stage 0, K tile, key block 0). S^T / dP^T rows:
+  // lane row l32, logical chunk 2 ks + h32. dQ^T transposed reads: the
+  // lo / hi rows 4 h + p / 4 (+ 8) of each 16-key half at head-dim block db.
+  // Other stages, the V tile, key blocks and key halves are whole multiples
+  // of 16 rows away, which keep the swizzle key, so they are immediates.
+  uint32_t rd[NKS], tr[NDB][2];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) rd[ks] = lds0 + (uint32_t)Tile::chunk(l32, 2 * ks + h32) * 16u;
+  {
+    const int pl = lane & 15, g = (lane >> 4) & 1;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi) {
+        const int r = 4 * h32 + (pl >> 2) + 8 * hi;
+        const int col = 32 * db + 16 * g + 4 * (pl & 3);
+        tr[db][hi] = lds0 + (uint32_t)Tile::elem(r, col) * 2u;
+      }
+  }
+
+  if (ntiles > 0) tile_load(0, 0);
   wait_all_memory();
   __syncthreads();
 
   const int wq0 = q0 + wave * 32;
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
-    if (it + 1 < ntiles) gload(it + 1);
-    const uint16_t* Ks = smem + buf * STAGE;
-    const uint16_t* Vs = Ks + KT;
+  // One tile on ring stage ST (a compile-time constant, so every LDS offset
+  // below is an immediate).
+  auto tile_body = [&](int it, auto stc) {
+    constexpr int ST = decltype(stc)::value;
+    if (it + 1 < ntiles) tile_load(it + 1, ST ^ 1);
     const int kbase = it * BN;
     const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && kbase + BN - 1 > wq0);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int kb0 = kbase + 32 * kb;
       if (CAUSAL && kb0 > wq0 + 31) continue;  // block entirely above the wave's rows
+      // S^T and dP^T as one stream of 2 NKS MFMA slots (slot m: k-step m / 2,
+      // S for even m, dP for odd), then dQ^T as NDQ slots (head-dim block
+      // j / 2, key half j % 2). Each slot issues the LDS read of the operand
+      // LA slots ahead (the last S/dP slots read the first dQ operands);
+      // fences keep that order, otherwise the reads trail by one slot and
+      // every MFMA waits for its operand.
+      constexpr int NSD = 2 * NKS;
+      constexpr int NDQ = 2 * NDB;
+      constexpr int LA = 4;
+      u32x4 op[NSD + NDQ];
+      auto read_op = [&](int m) {
+        if (m < NSD) {
+          const uint32_t off = ST * STAGE_B + ((m & 1) ? TB : 0) + kb * 32 * CPR * 16;
+          op[m] = *(const KF_LDS u32x4*)(uintptr_t)(rd[m >> 1] + off);
+        } else {
+          const int j = m - NSD;
+          const uint32_t off = ST * STAGE_B + (32 * kb + 16 * (j & 1)) * CPR * 16;
+          const u32x2 lo = lds_read_tr16_at(tr[j >> 1][0] + off);
+          const u32x2 hi = lds_read_tr16_at(tr[j >> 1][1] + off);
+          op[m] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+      };
       f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        const u32x4 a = lds_read16(Ks + (kb * 32 + l32) * KSTR + 16 * ks + 8 * h32);
-        s = Elem<T>::mfma(a, qf[ks], s);
-        const u32x4 a2 = lds_read16(Vs + (kb * 32 + l32) * VSTR + 16 * ks + 8 * h32);
-        dp = Elem<T>::mfma(a2, dof[ks], dp);
-      }
+      static_for<0, LA>([&](auto mc) { read_op(decltype(mc)::value); });
+      __builtin_amdgcn_sched_barrier(0);
+      static_for<0, NSD>([&](auto mc) {
+        constexpr int m = decltype(mc)::value;
+        if constexpr (m & 1)
+          dp = Elem<T>::mfma(op[m], dof[m >> 1], dp);
+        else
+          s = Elem<T>::mfma(op[m], qf[m >> 1], s);
+        if constexpr (m + LA < NSD + NDQ) read_op(m + LA);
+        __builtin_amdgcn_sched_barrier(0);
+      });
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = fmaf(s[r], p.scale_log2, -lse2);
       if (need_mask) {
@@ -283,16 +326,20 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) dp[r] = fast_exp2(s[r]) * (dp[r] - dlt);
       const u32x4 ds0 = pack8<T>(dp, 0), ds1 = pack8<T>(dp, 8);
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const u32x4 a = lds_read_tr_operand(Ks, KSTR, 32 * kb, 32 * db, lane);
-        dq[db] = Elem<T>::mfma(a, ds0, dq[db]);
-        const u32x4 a2 = lds_read_tr_operand(Ks, KSTR, 32 * kb + 16, 32 * db, lane);
-        dq[db] = Elem<T>::mfma(a2, ds1, dq[db]);
-      }
+      __builtin_amdgcn_sched_barrier(0);
+      static_for<0, NDQ>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        dq[j >> 1] = Elem<T>::mfma(op[NSD + j], (j & 1) ? ds1 : ds0, dq[j >> 1]);
+        if constexpr (NSD + j + LA < NSD + NDQ) read_op(NSD + j + LA);
+        __builtin_amdgcn_sched_barrier(0);
+      });
     }
-    if (it + 1 < ntiles) sstore(buf ^ 1);
-    __syncthreads();
+    KF_WAIT_VMCNT(0);  // this wave's loads of the next tile
+    __syncthreads();   // every wave's loads landed; stage ST is free again
+  };
+  for (int it = 0; it < ntiles; it += 2) {
+    tile_body(it, std::integral_constant<int, 0>{});
+    if (it + 1 < ntiles) tile_body(it + 1, std::integral_constant<int, 1>{});
   }
 
   if (row_ok) {
@@ -692,17 +739,19 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// 4. Fixup: one workgroup per key tile. Sums the partials of tiles shared by
-// several dkdv workgroups, zero-fills tiles that no query can see, and leaves
-// tiles one workgroup finished alone untouched.
+// 4. Fixup: kFixSub workgroups per key tile, 16 keys each. Sums the partials
+// of tiles shared by several dkdv workgroups, zero-fills tiles that no query
+// can see, and leaves tiles one workgroup finished alone untouched.
+constexpr int kFixSub = kBNK / 16;
 template <typename T, int DT, bool CAUSAL>
 __global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p) {
-  const int t = blockIdx.x;
+  const int t = blockIdx.x / kFixSub, sub = blockIdx.x % kFixSub;
   const int kt = t / p.ngroups, grp = t % p.ngroups;
   const int b = grp / p.Hkv, kvh = grp % p.Hkv;
-  const int k0 = kt * kBNK;
+  const int k0 = kt * kBNK + sub * 16;
   const int nq = dkdv_nq(kt, p.nqt, CAUSAL);
-  const int nkeys = min(kBNK, p.Sk - k0);
+  const int nkeys = min(16, p.Sk - k0);
+  if (nkeys <= 0) return;
   constexpr int QPR = DT / 4;
   if (nq == 0) {
     for (int e = threadIdx.x; e < nkeys * QPR; e += 256) {
@@ -722,7 +771,7 @@ __global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p) {
   const int64_t w0 = dkdv_owner(first, p.units, N), w1 = dkdv_owner(last, p.units, N);
   if (w0 == w1) return;
   for (int e = threadIdx.x; e < nkeys * QPR; e += 256) {
-    const int kr = e / QPR, d = (e % QPR) * 4;
+    const int kr = sub * 16 + e / QPR, d = (e % QPR) * 4;
     if (d >= p.D) continue;
     float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
     for (int64_t w = w0; w <= w1; ++w) {
@@ -738,10 +787,10 @@ __global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p) {
     u32x2 w2;
     w2[0] = pack2<T>(sk.x, sk.y);
     w2[1] = pack2<T>(sk.z, sk.w);
-    *reinterpret_cast<u32x2*>(p.dk + b * p.dk_sb + kvh * p.dk_sh + (k0 + kr) * p.dk_ss + d) = w2;
+    *reinterpret_cast<u32x2*>(p.dk + b * p.dk_sb + kvh * p.dk_sh + (kt * kBNK + kr) * p.dk_ss + d) = w2;
     w2[0] = pack2<T>(sv.x, sv.y);
     w2[1] = pack2<T>(sv.z, sv.w);
-    *reinterpret_cast<u32x2*>(p.dv + b * p.dv_sb + kvh * p.dv_sh + (k0 + kr) * p.dv_ss + d) = w2;
+    *reinterpret_cast<u32x2*>(p.dv + b * p.dv_sb + kvh * p.dv_sh + (kt * kBNK + kr) * p.dv_ss + d) = w2;
   }
 }
 
@@ -803,7 +852,7 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
     p.nqt = cdiv(p.Sq, kBMQ);
     p.nkt = cdiv(p.Sk, kBNK);
     p.units = dkdv_total_units(p.ngroups, p.G, p.nqt, p.nkt, causal);
-    const int64_t tiles = (int64_t)p.nkt * p.ngroups;
+    const int64_t tiles = (int64_t)p.nkt * p.ngroups * kFixSub;
     if (causal)
       hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, true>), dim3((unsigned)tiles), dim3(256), 0, stream, p);
     else

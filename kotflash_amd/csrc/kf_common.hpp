@@ -158,6 +158,12 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
+// The same read at an LDS byte address.
+__device__ inline u32x2 lds_read_tr16_at(uint32_t addr) {
+  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((KF_LDS s16x4*)(uintptr_t)addr);
+  return __builtin_bit_cast(u32x2, r);
+}
+
 // MFMA A operand of a transposed row-major LDS tile: lane (i = l % 32, h = l / 32)
 // receives X[row0 + 8u + 4h + e][col0 + i] for slots t = 4u + e.  The row index
 // of slot (h, t) is therefore 8 (t / 4) + 4 h + t % 4 -- the same contraction
