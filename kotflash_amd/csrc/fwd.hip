@@ -78,19 +78,15 @@ template <typename T, int DT, int QB, bool CAUSAL>
 __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdParams p) {
   constexpr int BM = 4 * QB * 32;
   constexpr int BN = 64;
-  // Row strides (elements). K is read by b128 rows (16 lanes per pass over 64
-  // four-byte banks): any stride of 16 mod 32 bytes is conflict-free. V is read
-  // transposed (32 lanes = 4 rows x 64 bytes per pass): a stride of 64 mod 128
-  // bytes puts the 4 rows on disjoint banks.
-  constexpr int KSTR = DT + 8;
-  constexpr int VSTR = DT + ((64 - 2 * DT) % 128 + 128) % 128 / 2;
-  constexpr int KT = BN * KSTR;
-  constexpr int STAGE = KT + BN * VSTR;
   constexpr int CPR = DT / 8;           // 16-byte chunks per row
-  constexpr int CPT = BN * CPR / 256;   // chunks per thread per tile and matrix
   constexpr int NKS = DT / 16;          // MFMA k-steps over head_dim
   constexpr int NDB = DT / 32;          // 32-wide head_dim blocks of O^T
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+  constexpr int TB = BN * DT * 2;       // bytes of one K (or V) tile
+  constexpr int STAGE_B = 2 * TB;       // K | V
+  constexpr int NKI = BN * CPR / 256;   // 1 KB loads per wave per tile and matrix
+  static_assert(BN * CPR == 256 * NKI, "tile chunks must split into whole loads");
+  using Tile = SwizzledTile<CPR>;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE_B / 2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
@@ -141,55 +137,63 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
   const int nkeys = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
   const int ntiles = cdiv(nkeys, BN);
 
-  // Per-thread load slots: chunk c covers (row e / CPR, column e % CPR) of the
-  // tile; the byte offsets only move by BN rows per tile.
-  uint32_t koff[CPT], voff[CPT];
-  int lrow[CPT];
+  // K/V tiles stream into a two-stage LDS ring by direct-to-LDS loads, stored
+  // unpadded with the swizzle of SwizzledTile (conflict-free for both the
+  // b128 row reads of K and the transposed reads of V). Per-lane load plan:
+  // for each of this wave's NKI 1 KB blocks of a tile, the byte offset of
+  // this lane's 16-byte chunk within the tile's rows (kOOB for head-dim
+  // padding); the tile's first key enters as soffset, and keys past Sk fall
+  // beyond the resource extent and load as zeros.
+  uint32_t koff[NKI], voff[NKI];
 #pragma unroll
-  for (int c = 0; c < CPT; ++c) {
-    const int e = tid + 256 * c;
-    const int row = e / CPR, col = e % CPR;
-    lrow[c] = row;
-    const bool colok = col * 8 < p.D;
-    koff[c] = colok ? (uint32_t)(row * p.k_ss + col * 8) * 2u : kOOB;
-    voff[c] = colok ? (uint32_t)(row * p.v_ss + col * 8) * 2u : kOOB;
+  for (int k = 0; k < NKI; ++k) {
+    const int pc = (wave * NKI + k) * 64 + lane;
+    const int r = pc / CPR;
+    const int c = (pc % CPR) ^ Tile::key(r);
+    const bool ok = c * 8 < p.D;
+    koff[k] = ok ? (uint32_t)(r * p.k_ss + c * 8) * 2u : kOOB;
+    voff[k] = ok ? (uint32_t)(r * p.v_ss + c * 8) * 2u : kOOB;
   }
-  const uint32_t kstep = (uint32_t)(BN * p.k_ss) * 2u, vstep = (uint32_t)(BN * p.v_ss) * 2u;
-
-  u32x4 kreg[CPT], vreg[CPT];
-  auto gload = [&](int tile) {
-    const int kbase = tile * BN;
+  const uint32_t lds0 = lds_addr(smem);
+  auto tile_load = [&](int tile, int st) {
+    const uint32_t kso = (uint32_t)(tile * BN * p.k_ss) * 2u;
+    const uint32_t vso = (uint32_t)(tile * BN * p.v_ss) * 2u;
+    const uint32_t m0 = lds0 + (uint32_t)st * STAGE_B + (uint32_t)(wave * NKI) * 1024u;
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const bool ok = kbase + lrow[c] < p.Sk;
-      kreg[c] = buf_load16(kr, ok ? koff[c] + (uint32_t)tile * kstep : kOOB);
-      vreg[c] = buf_load16(vr, ok ? voff[c] + (uint32_t)tile * vstep : kOOB);
+    for (int k = 0; k < NKI; ++k) {
+      dma16_s(kr, m0 + k * 1024u, koff[k], kso);
+      dma16_s(vr, m0 + TB + k * 1024u, voff[k], vso);
     }
   };
-  auto sstore = [&](int buf) {
-    uint16_t* Ks = smem + buf * STAGE;
-    uint16_t* Vs = Ks + KT;
+  // LDS read bases (bytes, stage 0, key block 0). K rows for S^T: lane row
+  // l32, logical chunk 2 ks + h32. V^T transposed reads: the lo / hi rows
+  // 4 h + p / 4 (+ 8) of a 16-key step at head-dim block db. Other stages,
+  // key blocks and key steps are whole multiples of 16 rows away, which keep
+  // the swizzle key, so they are immediate offsets.
+  uint32_t rd[NKS], trv[NDB][2];
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int e = tid + 256 * c;
-      const int row = e / CPR, col = e % CPR;
-      lds_write16(Ks + row * KSTR + col * 8, kreg[c]);
-      lds_write16(Vs + row * VSTR + col * 8, vreg[c]);
-    }
-  };
-
-  if (ntiles > 0) {
-    gload(0);
-    sstore(0);
+  for (int ks = 0; ks < NKS; ++ks) rd[ks] = lds0 + (uint32_t)Tile::chunk(l32, 2 * ks + h32) * 16u;
+  {
+    const int pl = lane & 15, g = (lane >> 4) & 1;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi) {
+        const int r = 4 * h32 + (pl >> 2) + 8 * hi;
+        const int col = 32 * db + 16 * g + 4 * (pl & 3);
+        trv[db][hi] = lds0 + TB + (uint32_t)Tile::elem(r, col) * 2u;
+      }
   }
+
+  if (ntiles > 0) tile_load(0, 0);
   wait_all_memory();
   __syncthreads();
 
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = it & 1;
-    if (it + 1 < ntiles) gload(it + 1);
-    const uint16_t* Ks = smem + buf * STAGE;
-    const uint16_t* Vs = Ks + KT;
+  // One tile on ring stage ST (a compile-time constant, so every LDS offset
+  // in the body is an immediate).
+  auto tile_body = [&](int it, auto stc) {
+    constexpr int ST = decltype(stc)::value;
+    if (it + 1 < ntiles) tile_load(it + 1, ST ^ 1);
     const int kbase = it * BN;
     // A causal tile whose first key is beyond every row of the wave is fully
     // masked for it.
@@ -205,9 +209,15 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
       constexpr int LA = 4;
       u32x4 kop[NS], vop[NPV];
       auto read_k = [&](int m) {
-        kop[m] = lds_read16(Ks + ((m / NKS) * 32 + l32) * KSTR + 16 * (m % NKS) + 8 * h32);
+        const uint32_t off = ST * STAGE_B + (m / NKS) * 32 * CPR * 16;
+        kop[m] = *(const KF_LDS u32x4*)(uintptr_t)(rd[m % NKS] + off);
       };
-      auto read_v = [&](int j) { vop[j] = lds_read_tr_operand(Vs, VSTR, 16 * (j % 4), 32 * (j / 4), lane); };
+      auto read_v = [&](int j) {
+        const uint32_t off = ST * STAGE_B + 16 * (j % 4) * CPR * 16;
+        const u32x2 lo = lds_read_tr16_at(trv[j / 4][0] + off);
+        const u32x2 hi = lds_read_tr16_at(trv[j / 4][1] + off);
+        vop[j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
       f32x16 s[QB][2];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
@@ -296,8 +306,12 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
         __builtin_amdgcn_sched_barrier(0);
       });
     }
-    if (it + 1 < ntiles) sstore(buf ^ 1);
-    __syncthreads();
+    KF_WAIT_VMCNT(0);  // this wave's loads of the next tile
+    __syncthreads();   // every wave's loads landed; stage ST is free again
+  };
+  for (int it = 0; it < ntiles; it += 2) {
+    tile_body(it, std::integral_constant<int, 0>{});
+    if (it + 1 < ntiles) tile_body(it + 1, std::integral_constant<int, 1>{});
   }
 
 #pragma unroll
