@@ -27,6 +27,8 @@
 //      number of fp32 partial copies plus a reduction pass (:198-332).
 // P and dS are rounded to the input dtype before the products that consume
 // them, as in the reference (:85, :183-184).
+#include <cstring>
+
 #include "kf_common.hpp"
 #include "kf_host.hpp"
 
@@ -79,10 +81,24 @@ __host__ __device__ inline int dkdv_nq(int kt, int nqt, bool causal) {
   const int n = nqt - dkdv_qstart(kt, causal);
   return n > 0 ? n : 0;
 }
-// Workgroup w owns units [floor(w U / N), floor((w + 1) U / N)).
-__host__ __device__ inline int64_t dkdv_u0(int64_t w, int64_t U, int64_t N) { return w * U / N; }
-__host__ __device__ inline int64_t dkdv_owner(int64_t u, int64_t U, int64_t N) {
-  return ((u + 1) * N + U - 1) / U - 1;
+// Stream-K shares: workgroup w owns units [start[w], start[w + 1]). The host
+// places the boundaries by cost rather than by unit count: every key-tile row
+// a workgroup enters (a "segment") costs about kSegmentCost units on top of
+// its units (loading the keys' K/V rows, filling the LDS ring, flushing the
+// accumulators), and the short rows of the causal triangle's far end would
+// otherwise pile many segments onto the last workgroups.
+constexpr int kMaxDkdvWG = 512;
+struct DkdvSplit {
+  int start[kMaxDkdvWG + 1];
+};
+// The workgroup that owns unit u (start[] is non-decreasing, start[0] = 0).
+__device__ inline int dkdv_owner(const DkdvSplit& sp, int nwg, int64_t u) {
+  int lo = 0, hi = nwg - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (sp.start[mid] <= u) lo = mid; else hi = mid - 1;
+  }
+  return lo;
 }
 
 // ---------------------------------------------------------------------------
@@ -374,7 +390,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
 //   dV^T += dO^T P,  dK^T += Q^T dS      (A = transposed LDS reads, B = P / dS
 //                                         straight from the S / dP registers)
 template <typename T, int DT, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
+__global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const DkdvSplit sp) {
   constexpr int CPR = DT / 8;
   constexpr int QT = kBMQ * DT;        // elements of one Q (or dO) tile
   constexpr int NQI = CPR / 4;         // 1 KB DMA instructions per wave per tile
@@ -393,9 +409,8 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
   const int lane = tid & 63, wave = wave_index();
   const int l32 = lane & 31, h32 = lane >> 5;
 
-  const int64_t N = gridDim.x;
-  int64_t u = dkdv_u0(blockIdx.x, p.units, N);
-  const int64_t uend = dkdv_u0(blockIdx.x + 1, p.units, N);
+  int64_t u = sp.start[blockIdx.x];
+  const int64_t uend = sp.start[blockIdx.x + 1];
   if (u >= uend) return;
 
   f32x16 dk[NDB], dv[NDB];
@@ -744,7 +759,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p) {
 // can see, and leaves tiles one workgroup finished alone untouched.
 constexpr int kFixSub = kBNK / 16;
 template <typename T, int DT, bool CAUSAL>
-__global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p) {
+__global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p, const DkdvSplit sp) {
   const int t = blockIdx.x / kFixSub, sub = blockIdx.x % kFixSub;
   const int kt = t / p.ngroups, grp = t % p.ngroups;
   const int b = grp / p.Hkv, kvh = grp % p.Hkv;
@@ -767,16 +782,15 @@ __global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p) {
   for (int k = 0; k < kt; ++k) base += (int64_t)p.ngroups * p.G * dkdv_nq(k, p.nqt, CAUSAL);
   const int64_t first = base + (int64_t)grp * p.G * nq;
   const int64_t last = first + (int64_t)p.G * nq - 1;
-  const int64_t N = p.nwg;
-  const int64_t w0 = dkdv_owner(first, p.units, N), w1 = dkdv_owner(last, p.units, N);
+  const int w0 = dkdv_owner(sp, p.nwg, first), w1 = dkdv_owner(sp, p.nwg, last);
   if (w0 == w1) return;
   for (int e = threadIdx.x; e < nkeys * QPR; e += 256) {
     const int kr = sub * 16 + e / QPR, d = (e % QPR) * 4;
     if (d >= p.D) continue;
     float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
-    for (int64_t w = w0; w <= w1; ++w) {
-      const int64_t wu0 = dkdv_u0(w, p.units, N);
-      if (dkdv_u0(w + 1, p.units, N) == wu0) continue;  // empty share: wrote nothing
+    for (int w = w0; w <= w1; ++w) {
+      const int64_t wu0 = sp.start[w];
+      if (sp.start[w + 1] == wu0) continue;  // empty share: wrote nothing
       const int side = wu0 >= first ? 0 : 1;
       const float* slot = p.part + (2 * w + side) * 2 * kBNK * DT + (int64_t)kr * DT + d;
       const float4 a = *reinterpret_cast<const float4*>(slot);
@@ -809,8 +823,59 @@ static int device_cu_count() {
   return n;
 }
 
+// One dK/dV workgroup per CU (each takes a whole CU's LDS).
+static int dkdv_workgroups() {
+  const int n = device_cu_count();
+  return n < kMaxDkdvWG ? n : kMaxDkdvWG;
+}
+
 static size_t delta_bytes(int64_t B, int64_t Hq, int64_t Sq) {
   return ((size_t)B * Hq * Sq * sizeof(float) + 255) / 256 * 256;
+}
+
+// Cost-weighted stream-K boundaries (see DkdvSplit). A segment start costs
+// kSegmentCost8 / 8 units; measured on the MI355X at config 3, a segment's
+// fixed cost is about 2.5 units.
+constexpr int kSegmentCost8 = 20;
+static void dkdv_split(DkdvSplit& sp, int ngroups, int G, int nqt, int nkt, bool causal, int nwg) {
+  struct Key {
+    int ngroups, G, nqt, nkt, causal, nwg;
+  };
+  thread_local Key last{-1, 0, 0, 0, 0, 0};
+  thread_local DkdvSplit cached;
+  const Key k{ngroups, G, nqt, nkt, causal ? 1 : 0, nwg};
+  if (memcmp(&k, &last, sizeof k) != 0) {
+    int64_t total = 0, all_units = 0;
+    for (int kt = 0; kt < nkt; ++kt) {
+      const int64_t units = (int64_t)G * dkdv_nq(kt, nqt, causal);
+      if (units) total += (int64_t)ngroups * (8 * units + kSegmentCost8);
+      all_units += (int64_t)ngroups * units;
+    }
+    int w = 1;
+    int64_t base = 0, cost = 0;
+    cached.start[0] = 0;
+    for (int kt = 0; kt < nkt && w < nwg; ++kt) {
+      const int64_t units = (int64_t)G * dkdv_nq(kt, nqt, causal);
+      if (!units) continue;
+      for (int g = 0; g < ngroups && w < nwg; ++g) {
+        const int64_t row_cost = 8 * units + kSegmentCost8;
+        // Boundaries whose target cost falls inside this tile row.
+        while (w < nwg) {
+          const int64_t target = (total * w + nwg - 1) / nwg;
+          if (target > cost + row_cost) break;
+          int64_t into = (target - cost - kSegmentCost8 + 7) / 8;
+          into = into < 0 ? 0 : (into > units ? units : into);
+          cached.start[w++] = (int)(base + into);
+        }
+        cost += row_cost;
+        base += units;
+      }
+    }
+    while (w < nwg) cached.start[w++] = (int)all_units;
+    cached.start[nwg] = (int)all_units;
+    last = k;
+  }
+  sp = cached;
 }
 
 static size_t partial_bytes(int nwg, int64_t D) {
@@ -841,10 +906,13 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
     p.nqt = cdiv(p.Sq, kBMQ);
     p.nkt = cdiv(p.Sk, kBNK);
     p.units = dkdv_total_units(p.ngroups, p.G, p.nqt, p.nkt, causal);
+    if (p.units > 0x7fffffff) return set_error(KF_EINVAL, "kf_attn_bwd: problem too large for one dK/dV launch");
+    DkdvSplit sp;
+    dkdv_split(sp, p.ngroups, p.G, p.nqt, p.nkt, causal, p.nwg);
     if (causal)
-      hipLaunchKernelGGL((dkdv_kernel<T, DT, true>), dim3((unsigned)p.nwg), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((dkdv_kernel<T, DT, true>), dim3((unsigned)p.nwg), dim3(256), 0, stream, p, sp);
     else
-      hipLaunchKernelGGL((dkdv_kernel<T, DT, false>), dim3((unsigned)p.nwg), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((dkdv_kernel<T, DT, false>), dim3((unsigned)p.nwg), dim3(256), 0, stream, p, sp);
     int rc = check_launch("kf_attn_bwd(dkdv)");
     if (rc) return rc;
   }
@@ -853,10 +921,12 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
     p.nkt = cdiv(p.Sk, kBNK);
     p.units = dkdv_total_units(p.ngroups, p.G, p.nqt, p.nkt, causal);
     const int64_t tiles = (int64_t)p.nkt * p.ngroups * kFixSub;
+    DkdvSplit sp;
+    dkdv_split(sp, p.ngroups, p.G, p.nqt, p.nkt, causal, p.nwg);
     if (causal)
-      hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, true>), dim3((unsigned)tiles), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, true>), dim3((unsigned)tiles), dim3(256), 0, stream, p, sp);
     else
-      hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, false>), dim3((unsigned)tiles), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, false>), dim3((unsigned)tiles), dim3(256), 0, stream, p, sp);
     int rc = check_launch("kf_attn_bwd(dkdv fixup)");
     if (rc) return rc;
   }
@@ -881,7 +951,7 @@ extern "C" size_t kf_attn_bwd_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv
                                               int64_t Sk, int64_t D, int causal) {
   (void)Hkv; (void)Sk; (void)causal;
   if (B <= 0 || Hq <= 0 || Sq <= 0 || D <= 0) return 0;
-  return 2 * delta_bytes(B, Hq, Sq) + partial_bytes(device_cu_count(), D);
+  return 2 * delta_bytes(B, Hq, Sq) + partial_bytes(dkdv_workgroups(), D);
 }
 
 extern "C" int kf_attn_bwd_stages(int stages, const void* q, const void* k, const void* v,
@@ -918,7 +988,7 @@ extern "C" int kf_attn_bwd_stages(int stages, const void* q, const void* k, cons
   p.q = (const uint16_t*)q; p.k = (const uint16_t*)k; p.v = (const uint16_t*)v;
   p.o = (const uint16_t*)o; p.dout = (const uint16_t*)dout; p.lse = lse;
   p.delta = (float*)workspace;
-  p.nwg = device_cu_count();
+  p.nwg = dkdv_workgroups();
   p.lse2 = (float*)((char*)workspace + delta_bytes(B, Hq, Sq));
   p.part = (float*)((char*)workspace + 2 * delta_bytes(B, Hq, Sq));
   p.dq = (uint16_t*)dq; p.dk = (uint16_t*)dk; p.dv = (uint16_t*)dv;
