@@ -834,9 +834,10 @@ static size_t delta_bytes(int64_t B, int64_t Hq, int64_t Sq) {
 }
 
 // Cost-weighted stream-K boundaries (see DkdvSplit). A segment start costs
-// kSegmentCost8 / 8 units; measured on the MI355X at config 3, a segment's
-// fixed cost is about 2.5 units.
-constexpr int kSegmentCost8 = 20;
+// kSegmentCost8 / 8 units: on the MI355X at config 3 a segment's fixed cost
+// came out at 2.5 units from per-workgroup timestamps, and a sweep of the
+// weight put the shortest launch at 4.5 to 6 units.
+constexpr int kSegmentCost8 = 40;
 static void dkdv_split(DkdvSplit& sp, int ngroups, int G, int nqt, int nkt, bool causal, int nwg) {
   struct Key {
     int ngroups, G, nqt, nkt, causal, nwg;
