@@ -2,30 +2,37 @@
 //
 // Layout of the work:
 //  * The Hq/Hkv query heads of a KV group and the Sq query positions are packed
-//    into R = G * Sq rows (row = g * Sq + i). A workgroup owns up to 32 * QB of
-//    those rows for one (batch, kv_head) and one KV chunk, so every K/V byte of
-//    the chunk is read from HBM once for all rows of the group (the reference
-//    re-reads K/V once per query head, triton_decode.py:16-104).
+//    into R = G * Sq rows (row = g * Sq + i). A workgroup owns up to 16 * QB of
+//    those rows (QB = 1, 2, 4) for one (batch, kv_head) and one KV chunk, so
+//    every K/V byte of the chunk is read from HBM once for all rows of the
+//    group (the reference re-reads K/V once per query head,
+//    triton_decode.py:16-104). Rows come in 16-row blocks because the products
+//    are v_mfma_f32_16x16x32: a decode step has few rows (4 at G = 4, Sq = 1),
+//    of which a 16-row block computes a quarter usefully and a 32-row block an
+//    eighth, so 16-row blocks take half as long per key.
 //  * The chunk is cut into 32-key steps that the 4 waves take in turn (so
 //    chunks are whole 128-key granules). Each wave streams its own steps with
 //    no workgroup barrier: its K and V tiles go into a wave-private LDS ring
 //    by direct-to-LDS loads (two steps in flight), and the wave keeps its own
 //    online-softmax state
 //    (S^T = K Q^T per step, P^T feeding O^T += V^T P^T as in the forward).
+//    The Q tile is loaded the same way, so a wave starts on its first step as
+//    soon as that step has landed while its later loads are still in flight.
 //  * At the end the 4 per-wave states are merged in LDS in one pass with a
 //    fixed order (deterministic), and the workgroup writes either the final
 //    O/LSE (one split) or an fp32 partial (O_s, LSE_s) of its row block.
 //  * Keys at or beyond the per-batch visible length L_b are masked; a split
 //    with no visible key writes O_s = 0, LSE_s = -inf (weight 0 in the merge),
 //    as the reference does (triton_forward.py:240-246).
-//  * merge_kernel (second launch, one workgroup per output row) combines the
+//  * merge_kernel (second launch, one wave per output row) combines the
 //    partials with LSE weights
 //      w_s = exp(LSE_s - max) / sum_t exp(LSE_t - max),  LSE = max + ln(sum)
-//    guarded for all -inf (reference triton_forward.py:269-349). Each of its
-//    threads issues all of its partial loads before using any, so the merge
-//    costs about one memory latency. (A single-launch merge by the last
-//    arriving workgroup needs an agent-scope release fence per workgroup; on
-//    this part those fences cost more than the second launch.)
+//    guarded for all -inf (reference triton_forward.py:269-349). Each lane
+//    issues all of its partial loads before using any, so the merge costs
+//    about one memory latency. (A single-launch merge by the last arriving
+//    workgroup was measured slower: either agent-scope release fences or
+//    agent-scope stores plus a counter atomic per workgroup cost more than
+//    the second launch.)
 #include "kf_common.hpp"
 #include "kf_host.hpp"
 
@@ -60,25 +67,28 @@ constexpr int kDecGranule = 128;
 
 template <typename T, int DT, int QB>
 __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
-  constexpr int CPR = DT / 8;
-  constexpr int NKS = DT / 16;
-  constexpr int NDB = DT / 32;
-  constexpr int RB = 32 * QB;          // rows per workgroup
+  constexpr int CPR = DT / 8;          // 16-byte chunks per row
+  constexpr int NDC = DT / 32;         // 32-wide head-dim chunks (S contraction)
+  constexpr int NDB = DT / 16;         // 16-wide head-dim blocks of O^T
+  constexpr int RB = 16 * QB;          // packed rows per workgroup
   constexpr int RING = 2;              // 32-key steps in flight per wave
   constexpr int VT = 32 * DT;          // elements of one K (or V) step tile
   constexpr int NVI = 32 * CPR / 64;   // 1 KB DMA instructions per step tile
   constexpr int NL = 2 * NVI;          // memory instructions per step (K and V)
+  constexpr int QT = RB * DT;          // elements of the Q tile
+  constexpr int NQI = RB * CPR / 64;   // DMA instructions of the Q tile
   constexpr int OSTR = DT + 1;         // padded rows of the merge buffer
   using Tile = SwizzledTile<CPR>;
-  static_assert(32 * CPR % 64 == 0, "V step tiles must split into whole DMA instructions");
-  // Per wave: RING (K, V) step tiles; reused at the end for the cross-wave merge.
-  constexpr int VBYTES = 4 * RING * 2 * VT * 2;
+  static_assert(32 * CPR % 64 == 0 && RB * CPR % 64 == 0, "tiles must split into whole DMA instructions");
+  // Q tile, then per wave RING (K, V) step tiles; reused at the end for the
+  // cross-wave merge.
+  constexpr int VBYTES = (QT + 4 * RING * 2 * VT) * 2;
   constexpr int MBYTES = (4 * RB * OSTR + 8 * RB) * 4;
   __shared__ __attribute__((aligned(16))) uint8_t smem[VBYTES > MBYTES ? VBYTES : MBYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
-  const int l32 = lane & 31, h32 = lane >> 5;
+  const int l16 = lane & 15, g16 = lane >> 4;
 
   int bid = blockIdx.x;
   const int split = bid % p.nsplit;
@@ -95,96 +105,137 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   // This wave's steps: 32-key blocks c0 + 32 (wave + 4 j), j = 0 .. nst - 1.
   const int nst = c1 > c0 + 32 * wave ? cdiv(c1 - c0 - 32 * wave, 128) : 0;
 
-  const auto kr = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, rows_extent(p.Sk, p.k_ss, p.D));
-  const auto vr = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, rows_extent(p.Sk, p.v_ss, p.D));
-  uint16_t* kvring = reinterpret_cast<uint16_t*>(smem) + wave * RING * 2 * VT;  // [slot][K | V]
+  // K/V resources end at the chunk's last visible key: keys at or beyond c1
+  // (the range check includes the scalar offset) load as zeros.
+  const auto kr = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, rows_extent(c1, p.k_ss, p.D));
+  const auto vr = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, rows_extent(c1, p.v_ss, p.D));
+  const auto qr = make_rsrc(p.q + b * p.q_sb + kvh * p.G * p.q_sh,
+                            (uint32_t)((((int64_t)p.G - 1) * p.q_sh + ((int64_t)p.Sq - 1) * p.q_ss + p.D) * 2));
+  uint16_t* qs = reinterpret_cast<uint16_t*>(smem);                 // [RB][DT], swizzled
+  uint16_t* kvring = qs + QT + wave * RING * 2 * VT;                // [slot][K | V]
 
-  // Q rows as MFMA B operands (lane = packed row).
-  u32x4 qf[QB][NKS];
+  // The Q tile goes to LDS by direct-to-LDS loads too (the waves share its
+  // instructions), so that no register load is pending when the ring starts:
+  // the compiler would otherwise wait for every load at the first use of Q.
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int rho = rb * RB + qb * 32 + l32;
-    const bool ok = rho < R;
+  for (int k = 0; k < NQI; ++k) {
+    if (k % 4 != wave) continue;
+    const int pc = k * 64 + lane;
+    const int r = pc / CPR;
+    const int c = (pc % CPR) ^ Tile::key(r);
+    const int rho = rb * RB + r;
+    const bool ok = rho < R && c * 8 < p.D;
     const int g = ok ? rho / p.Sq : 0, i = ok ? rho % p.Sq : 0;
-    const auto qr = make_rsrc(p.q + b * p.q_sb + kvh * p.G * p.q_sh,
-                              (uint32_t)((((int64_t)p.G - 1) * p.q_sh + ((int64_t)p.Sq - 1) * p.q_ss + p.D) * 2));
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      const int d = 16 * ks + 8 * h32;
-      qf[qb][ks] = buf_load16(qr, (ok && d < p.D) ? (uint32_t)(g * p.q_sh + i * p.q_ss + d) * 2u : kOOB);
-    }
+    dma16(qr, qs + k * 512, ok ? (uint32_t)(g * p.q_sh + i * p.q_ss + c * 8) * 2u : kOOB);
   }
-  const float sl2 = fabsf(p.scale_log2);
-  // Per-lane DMA plan: the tile row this lane fills in each instruction
-  // (huge for head-dim padding) and its chunk's byte offset in the row.
-  int vrow[NVI];
-  uint32_t vcol[NVI];
+  // Per-lane DMA plan of a K/V step tile: the byte offset of this lane's
+  // 16-byte chunk within the tile's rows (kOOB for head-dim padding). The
+  // step's first key enters as the scalar offset, so issuing a step costs no
+  // vector instructions.
+  uint32_t koff[NVI], voff[NVI];
 #pragma unroll
   for (int k = 0; k < NVI; ++k) {
     const int pc = k * 64 + lane;
     const int r = pc / CPR;
     const int c = (pc % CPR) ^ Tile::key(r);
-    vrow[k] = c * 8 < p.D ? r : 0x7fffffff;
-    vcol[k] = (uint32_t)c * 16u;
+    const bool ok = c * 8 < p.D;
+    koff[k] = ok ? (uint32_t)(r * p.k_ss + c * 8) * 2u : kOOB;
+    voff[k] = ok ? (uint32_t)(r * p.v_ss + c * 8) * 2u : kOOB;
   }
+  const uint32_t ring0 = lds_addr(kvring);
   // Step j of this wave: its K and V tiles (32 keys) into the wave's LDS
-  // ring by direct-to-LDS loads. Every load of the loop is of this kind, so
-  // the compiler tracks none of them and the explicit waits below are the
-  // only ones (a compiler wait on a register load would drain the ring).
+  // ring. Every load of the kernel is a direct-to-LDS load, so the explicit
+  // waits below are the only ones.
   auto issue = [&](int j, auto slot_c) {
     constexpr int slot = decltype(slot_c)::value;
     const int kb0 = c0 + 32 * (wave + 4 * j);
+    const uint32_t kso = (uint32_t)kb0 * (uint32_t)(p.k_ss * 2);
+    const uint32_t vso = (uint32_t)kb0 * (uint32_t)(p.v_ss * 2);
+    const uint32_t m0 = ring0 + (uint32_t)(slot * 2 * VT * 2);
 #pragma unroll
     for (int k = 0; k < NVI; ++k) {
-      const bool ok = vrow[k] < c1 - kb0;
-      const uint32_t row = (uint32_t)(kb0 + vrow[k]);
-      dma16(kr, kvring + slot * 2 * VT + k * 512, ok ? row * (uint32_t)(p.k_ss * 2) + vcol[k] : kOOB);
-      dma16(vr, kvring + slot * 2 * VT + VT + k * 512, ok ? row * (uint32_t)(p.v_ss * 2) + vcol[k] : kOOB);
+      dma16_s(kr, m0 + k * 1024u, koff[k], kso);
+      dma16_s(vr, m0 + VT * 2 + k * 1024u, voff[k], vso);
     }
   };
+  static_for<0, RING>([&](auto sc) {
+    if (decltype(sc)::value < nst) issue(decltype(sc)::value, sc);
+  });
 
-  f32x16 oacc[QB][NDB];
+  f32x4 oacc[QB][NDB];  // O^T: lane l, register r = head-dim 16 db + 4 (l / 16) + r of row l % 16
   float m_i[QB], l_i[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     m_i[qb] = kNegInf;
     l_i[qb] = 0.f;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) oacc[qb][db] = zero16();
+    for (int db = 0; db < NDB; ++db) oacc[qb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // One 32-key step from ring slot `slot`.
+  // Q and step 0 have landed once at most one later step is outstanding (the
+  // counter completes in order); the barrier publishes every wave's share of
+  // the Q tile. Waves without steps pass it too.
+  if (nst >= 2) KF_WAIT_VMCNT(NL);
+  else KF_WAIT_VMCNT(0);
+  __syncthreads();
+  // Q rows as MFMA B operands: lane l = packed row qb * 16 + l % 16, k slots =
+  // head dims 32 dc + 8 (l / 16) .. + 7.
+  u32x4 qf[QB][NDC];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+    for (int dc = 0; dc < NDC; ++dc) qf[qb][dc] = lds_read16(qs + Tile::chunk(qb * 16 + l16, 4 * dc + g16) * 8);
+  const float sl2 = fabsf(p.scale_log2);
+  // Scores are reduced before scaling, which needs a positive scale: for a
+  // negative one Q is negated (exact) and |scale| (sl2) used.
+  if (p.scale_log2 < 0.f) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int dc = 0; dc < NDC; ++dc) qf[qb][dc] ^= 0x80008000u;
+  }
+
+  // One 32-key step from ring slot `slot`, as two 16-key blocks kb.
   auto step = [&](int j, auto slot_c) {
     constexpr int slot = decltype(slot_c)::value;
     const int kb0 = c0 + 32 * (wave + 4 * j);
     const uint16_t* Ks = kvring + slot * 2 * VT;
     const uint16_t* Vs = Ks + VT;
-    u32x4 ka[NKS];  // K rows as MFMA A operands: lane = key, slots = head_dim
+    // K rows as MFMA A operands: lane = key kb * 16 + l % 16, slots = head dims.
+    u32x4 ka[2][NDC];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) ka[ks] = lds_read16(Ks + Tile::chunk(l32, 2 * ks + h32) * 8);
-    f32x16 s[QB];
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      s[qb] = zero16();
+      for (int dc = 0; dc < NDC; ++dc) ka[kb][dc] = lds_read16(Ks + Tile::chunk(kb * 16 + l16, 4 * dc + g16) * 8);
+    // S^T: lane l, register r = key kb * 16 + 4 (l / 16) + r of row l % 16.
+    f32x4 s[QB][2];
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) s[qb] = Elem<T>::mfma(ka[ks], qf[qb][ks], s[qb]);
-    }
-    // S^T layout: lane = row, register r = key kb0 + 8 (r/4) + 4 h + r % 4.
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        s[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dc = 0; dc < NDC; ++dc) s[qb][kb] = Elem<T>::mfma16(ka[kb][dc], qf[qb][dc], s[qb][kb]);
+      }
     const int lim = c1 - kb0;  // keys c < lim are visible
-    u32x4 pk[QB][2];
+    u32x4 pk[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       if (lim < 32) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int c = 8 * (r >> 2) + 4 * h32 + (r & 3);
-          s[qb][r] = c < lim ? s[qb][r] : kNegInf;
-        }
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int c = 16 * kb + 4 * g16 + r;
+            s[qb][kb][r] = c < lim ? s[qb][kb][r] : kNegInf;
+          }
       }
       float mx = kNegInf;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qb][r]);
-      mx = wave_xor32_max(mx) * sl2;
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[qb][kb][r]);
+      mx = wave_group16_max(mx) * sl2;
       if (m_i[qb] == kNegInf) {
         m_i[qb] = mx;
       } else {
@@ -199,49 +250,36 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
       }
       const float msub = (m_i[qb] == kNegInf) ? 0.f : m_i[qb];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[qb][r] = fast_exp2(fmaf(s[qb][r], sl2, -msub));
-      pk[qb][0] = pack8<T>(s[qb], 0);
-      pk[qb][1] = pack8<T>(s[qb], 8);
-      // The denominator sums the rounded P that the PV product consumes.
-      float rs0 = 0.f, rs1 = 0.f;
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int w2 = 0; w2 < 2; ++w2) {
-        rs0 = sum2_acc<T>(pk[qb][w2][0], rs0);
-        rs1 = sum2_acc<T>(pk[qb][w2][1], rs1);
-        rs0 = sum2_acc<T>(pk[qb][w2][2], rs0);
-        rs1 = sum2_acc<T>(pk[qb][w2][3], rs1);
-      }
-      l_i[qb] += rs0 + rs1;
+        for (int r = 0; r < 4; ++r) s[qb][kb][r] = fast_exp2(fmaf(s[qb][kb][r], sl2, -msub));
+      // P^T as the B operand of O^T += V^T P^T: slot t of lane group g holds
+      // key 4 g + t (t < 4) or 16 + 4 g + t - 4 (t >= 4).
+      pk[qb][0] = pack2<T>(s[qb][0][0], s[qb][0][1]);
+      pk[qb][1] = pack2<T>(s[qb][0][2], s[qb][0][3]);
+      pk[qb][2] = pack2<T>(s[qb][1][0], s[qb][1][1]);
+      pk[qb][3] = pack2<T>(s[qb][1][2], s[qb][1][3]);
+      // The denominator sums the rounded P that the PV product consumes.
+      l_i[qb] += sum2_acc<T>(pk[qb][0], sum2_acc<T>(pk[qb][1], 0.f)) +
+                 sum2_acc<T>(pk[qb][2], sum2_acc<T>(pk[qb][3], 0.f));
     }
+    // V^T A operands by transposed reads: lane (g, i) receives V[key][16 db + i]
+    // for the keys of slot t above (rows 4 g .. 4 g + 3 and 16 + 4 g .. + 3).
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
+      const int col = 16 * db + 4 * (l16 & 3);
+      const u32x2 lo = lds_read_tr16(Vs + Tile::elem(4 * g16 + (l16 >> 2), col));
+      const u32x2 hi = lds_read_tr16(Vs + Tile::elem(16 + 4 * g16 + (l16 >> 2), col));
+      const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-      for (int stp = 0; stp < 2; ++stp) {
-        const u32x4 a = lds_read_tr_operand_sw<CPR>(Vs, 16 * stp, 32 * db, lane);
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) oacc[qb][db] = Elem<T>::mfma(a, pk[qb][stp], oacc[qb][db]);
-      }
+      for (int qb = 0; qb < QB; ++qb) oacc[qb][db] = Elem<T>::mfma16(a, pk[qb], oacc[qb][db]);
     }
   };
 
   // Ring: steps j .. j + RING - 1 are in flight; before step j the wave waits
   // for its loads (those of later steps may remain outstanding), and after it
-  // refills the slot with step j + RING. A wave only ever reads its own LDS
+  // refills the slot with step j + RING. A wave only ever reads its own ring
   // slots, so no workgroup barrier is needed until the merge.
-  static_for<0, RING>([&](auto sc) {
-    if (decltype(sc)::value < nst) issue(decltype(sc)::value, sc);
-  });
-  // Q (issued first) is needed from the first step on; waiting for it only
-  // now overlaps its latency with that of the ring's first loads.
-  wait_all_memory();
-  // Scores are reduced before scaling, which needs a positive scale: for a
-  // negative one Q is negated (exact) and |scale| (sl2) used.
-  if (p.scale_log2 < 0.f) {
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) qf[qb][ks] ^= 0x80008000u;
-  }
   for (int j0 = 0; j0 < nst; j0 += RING) {
     static_for<0, RING>([&](auto sc) {
       constexpr int slot = decltype(sc)::value;
@@ -259,28 +297,29 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
 
   // Cross-wave merge in one pass: every wave stores (m, l, O) of its rows;
   // then each output element combines the four waves in a fixed order.
-  __syncthreads();  // all waves are done with their V rings
+  __syncthreads();  // all waves are done with the Q tile and their rings
   float* obuf = reinterpret_cast<float*>(smem);  // [4][RB][OSTR]
   float* mbuf = obuf + 4 * RB * OSTR;            // [4][RB]
   float* lbuf = mbuf + 4 * RB;                   // [4][RB]
+  const int nrow = min(RB, R - rb * RB);
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
-    const int r = qb * 32 + l32;
-    const float lt = wave_xor32_sum(l_i[qb]);
-    if (h32 == 0) {
+    if (qb * 16 >= nrow) break;
+    const int r = qb * 16 + l16;
+    const float lt = wave_group16_sum(l_i[qb]);
+    if (g16 == 0) {
       mbuf[wave * RB + r] = m_i[qb];
       lbuf[wave * RB + r] = lt;
     }
-    float* orow = obuf + (wave * RB + r) * OSTR;
+    float* orow = obuf + (wave * RB + r) * OSTR + 4 * g16;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr) orow[32 * db + 8 * (rr >> 2) + 4 * h32 + (rr & 3)] = oacc[qb][db][rr];
+      for (int rr = 0; rr < 4; ++rr) orow[16 * db + rr] = oacc[qb][db][rr];
   }
   __syncthreads();
 
   // Output: final O/LSE (one split) or this split's fp32 partial.
-  const int nrow = min(RB, R - rb * RB);
   const int DQ = p.D / 4;
   const int grp = (b * p.Hkv + kvh) * p.nrb + rb;
   const int64_t pbase = ((int64_t)grp * p.nsplit + split) * RB;
@@ -318,16 +357,20 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   }
 }
 
-// Merge of the split partials: one workgroup per output row. Thread
-// (q = tid % DQ, sl = tid / DQ) owns 4 columns of splits sl, sl + SL, ...; it
-// issues the loads of up to kMergeU of its splits (LSE and O) before using
-// any, so a chunk of kMergeU * SL splits costs one memory round trip: the
-// common case (nsplit <= kMergeU * SL) reads everything in one trip.
-constexpr int kMergeU = 8;
+// Merge of the split partials: one wave per output row, no LDS and no
+// barrier. Lane l = (q = l % QL, sl = l / QL) owns the 4 head-dim columns
+// 4q .. 4q + 3 (QL = 16 or 32 lanes cover D / 4 <= QL) of splits sl, sl + SW,
+// sl + 2 SW, ... (SW = 64 / QL). Its loads are buffer loads whose
+// out-of-range lanes read zero, so no branch separates them and all kMergeU
+// of a chunk (O and LSE) are in flight before the first is used: the common
+// case (nsplit <= kMergeU * SW) costs one memory round trip. The SW lanes of
+// a column then combine with lane swaps (v_permlane16/32_swap).
+constexpr int kMergeU = 16;
 
-template <typename T>
-__global__ __launch_bounds__(256) void merge_kernel(const DecParams p) {
-  const int tid = threadIdx.x;
+template <typename T, int QL>
+__global__ __launch_bounds__(64) void merge_kernel(const DecParams p) {
+  constexpr int SW = 64 / QL;
+  const int lane = threadIdx.x;
   const int RB = p.rb_rows;
   const int R = p.G * p.Sq;
   // blockIdx -> (b, kvh, packed row rho); partial rows are grouped by row block.
@@ -338,98 +381,100 @@ __global__ __launch_bounds__(256) void merge_kernel(const DecParams p) {
   const int grp = (b * p.Hkv + kvh) * p.nrb + rb;
   const int g = rho_all / p.Sq, i = rho_all % p.Sq;
   const int h = kvh * p.G + g;
-  const float* plse = p.part_lse + (int64_t)grp * p.nsplit * RB + r;
-  const float* po = p.part_o + (int64_t)grp * p.nsplit * RB * p.D + (int64_t)r * p.D;
-  __shared__ float red[8];
-  __shared__ float4 acc4[256];
-
-  const int DQ = p.D / 4;
-  const int SL = 256 / DQ;
-  const int q = tid % DQ, sl = tid / DQ;
-  const bool active = sl < SL;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  float den = 0.f, mrun = kNegInf;  // running reference max of this thread's chunks
-  for (int c0 = 0; c0 < p.nsplit; c0 += kMergeU * SL) {
-    float4 v[kMergeU];
+  // Row r of every split's partial: O at (s * RB + r) * D floats, LSE at s * RB + r.
+  const auto orr = make_rsrc(p.part_o + ((int64_t)grp * p.nsplit * RB + r) * p.D,
+                             (uint32_t)(((int64_t)(p.nsplit - 1) * RB * p.D + p.D) * 4));
+  const auto lrr = make_rsrc(p.part_lse + (int64_t)grp * p.nsplit * RB + r,
+                             (uint32_t)(((int64_t)(p.nsplit - 1) * RB + 1) * 4));
+  const int q = lane % QL, sl = lane / QL;
+  const bool col = 4 * q < p.D;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float den = 0.f, mrun = kNegInf;  // running reference max of this lane's chunks (log2 units)
+  for (int c0 = 0; c0 < p.nsplit; c0 += kMergeU * SW) {
+    u32x4 v[kMergeU];
     float w[kMergeU];
+    uint32_t lw[kMergeU];
 #pragma unroll
     for (int u = 0; u < kMergeU; ++u) {
-      const int s2 = c0 + sl + SL * u;
-      const bool ok = active && s2 < p.nsplit;
-      v[u] = ok ? *reinterpret_cast<const float4*>(po + (int64_t)s2 * RB * p.D + 4 * q)
-                : make_float4(0.f, 0.f, 0.f, 0.f);
-      w[u] = ok ? plse[(int64_t)s2 * RB] * kLog2e : kNegInf;
+      const int s2 = c0 + sl + SW * u;
+      lw[u] = __builtin_amdgcn_raw_buffer_load_b32(lrr, s2 < p.nsplit ? (uint32_t)(s2 * RB) * 4u : kOOB, 0, 0);
     }
+#pragma unroll
+    for (int u = 0; u < kMergeU; ++u) {
+      const int s2 = c0 + sl + SW * u;
+      v[u] = buf_load16(orr, s2 < p.nsplit && col ? (uint32_t)(s2 * RB * p.D + 4 * q) * 4u : kOOB);
+    }
+    // Keep every load of the chunk ahead of the first use: left alone, the
+    // scheduler recycles early result registers and waits for them mid-batch.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kMergeU; ++u)
+      w[u] = c0 + sl + SW * u < p.nsplit ? __uint_as_float(lw[u]) * kLog2e : kNegInf;
     float mx = kNegInf;
 #pragma unroll
     for (int u = 0; u < kMergeU; ++u) mx = fmaxf(mx, w[u]);
-    // Thread-local online rescale across chunks (one chunk in the common case).
+    // Lane-local online rescale across chunks (one chunk in the common case).
     const float mnew = fmaxf(mrun, mx);
     const float ms = mnew == kNegInf ? 0.f : mnew;
     const float alpha = fast_exp2(mrun - ms);
-    acc.x *= alpha; acc.y *= alpha; acc.z *= alpha; acc.w *= alpha;
+    acc *= alpha;
     den *= alpha;
 #pragma unroll
     for (int u = 0; u < kMergeU; ++u) {
       const float wt = fast_exp2(w[u] - ms);
       den += wt;
-      acc.x += wt * v[u].x; acc.y += wt * v[u].y; acc.z += wt * v[u].z; acc.w += wt * v[u].w;
+      acc[0] += wt * __uint_as_float(v[u][0]); acc[1] += wt * __uint_as_float(v[u][1]);
+      acc[2] += wt * __uint_as_float(v[u][2]); acc[3] += wt * __uint_as_float(v[u][3]);
     }
     mrun = mnew;
   }
-  // Block-wide max of the per-thread reference maxima, then rescale.
-  float mx = mrun;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-  if ((tid & 63) == 0) red[tid >> 6] = mx;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // Combine the SW split lanes of each column: common reference max, then sums.
+  const float M = QL == 16 ? wave_group16_max(mrun) : wave_xor32_max(mrun);
   const float Ms = M == kNegInf ? 0.f : M;
   const float sc = fast_exp2(mrun - Ms);
-  acc.x *= sc; acc.y *= sc; acc.z *= sc; acc.w *= sc;
-  den *= sc;
-  // Every split's weight was counted once per column group; use q == 0's.
-  float dsum = q == 0 ? den : 0.f;
+  float dtot = den * sc;
+  dtot = QL == 16 ? wave_group16_sum(dtot) : wave_xor32_sum(dtot);
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) dsum += __shfl_xor(dsum, off);
-  __syncthreads();
-  if ((tid & 63) == 0) red[4 + (tid >> 6)] = dsum;
-  acc4[tid] = acc;
-  __syncthreads();
-  const float dtot = red[4] + red[5] + red[6] + red[7];
-  if (tid < DQ) {
-    for (int s2 = 1; s2 < SL; ++s2) {
-      const float4 o2 = acc4[s2 * DQ + tid];
-      acc.x += o2.x; acc.y += o2.y; acc.z += o2.z; acc.w += o2.w;
-    }
+  for (int e = 0; e < 4; ++e) {
+    const float x = acc[e] * sc;
+    acc[e] = QL == 16 ? wave_group16_sum(x) : wave_xor32_sum(x);
+  }
+  if (sl == 0 && col) {
     const float inv = dtot > 0.f ? 1.f / dtot : 0.f;
     u32x2 wv;
-    wv[0] = pack2<T>(acc.x * inv, acc.y * inv);
-    wv[1] = pack2<T>(acc.z * inv, acc.w * inv);
-    *reinterpret_cast<u32x2*>(p.o + b * p.o_sb + h * p.o_sh + i * p.o_ss + 4 * tid) = wv;
-    if (tid == 0 && p.lse)
+    wv[0] = pack2<T>(acc[0] * inv, acc[1] * inv);
+    wv[1] = pack2<T>(acc[2] * inv, acc[3] * inv);
+    *reinterpret_cast<u32x2*>(p.o + b * p.o_sb + h * p.o_sh + i * p.o_ss + 4 * q) = wv;
+    if (q == 0 && p.lse)
       p.lse[((int64_t)b * p.Hq + h) * p.Sq + i] = dtot > 0.f ? (M + fast_log2(dtot)) * kLn2 : kNegInf;
   }
 }
 
-static int decode_rows_per_wg(int64_t G, int64_t Sq) { return G * Sq <= 32 ? 32 : 64; }
+// Packed rows per workgroup: 16-row MFMA blocks, up to four of them.
+static int decode_rows_per_wg(int64_t G, int64_t Sq) {
+  const int64_t R = G * Sq;
+  return R <= 16 ? 16 : R <= 32 ? 32 : 64;
+}
 
 template <typename T, int DT>
 static int launch_decode(DecParams p, hipStream_t stream) {
   const int R = p.G * p.Sq;
-  const bool qb2 = R > 32;
-  p.rb_rows = qb2 ? 64 : 32;
+  p.rb_rows = decode_rows_per_wg(p.G, p.Sq);
   p.nrb = cdiv(R, p.rb_rows);
   const int64_t grid = (int64_t)p.nsplit * p.nrb * p.B * p.Hkv;
   if (grid > 0x7fffffff) return set_error(KF_EUNSUPPORTED, "kf_attn_decode: grid too large");
-  if (qb2)
-    hipLaunchKernelGGL((decode_kernel<T, DT, 2>), dim3((unsigned)grid), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL((decode_kernel<T, DT, 1>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  switch (p.rb_rows) {
+    case 16: hipLaunchKernelGGL((decode_kernel<T, DT, 1>), dim3((unsigned)grid), dim3(256), 0, stream, p); break;
+    case 32: hipLaunchKernelGGL((decode_kernel<T, DT, 2>), dim3((unsigned)grid), dim3(256), 0, stream, p); break;
+    default: hipLaunchKernelGGL((decode_kernel<T, DT, 4>), dim3((unsigned)grid), dim3(256), 0, stream, p); break;
+  }
   int rc = check_launch("kf_attn_decode(split)");
   if (rc || p.nsplit == 1) return rc;
   const int64_t mgrid = (int64_t)p.B * p.Hkv * R;
-  hipLaunchKernelGGL((merge_kernel<T>), dim3((unsigned)mgrid), dim3(256), 0, stream, p);
+  if (p.D <= 64)
+    hipLaunchKernelGGL((merge_kernel<T, 16>), dim3((unsigned)mgrid), dim3(64), 0, stream, p);
+  else
+    hipLaunchKernelGGL((merge_kernel<T, 32>), dim3((unsigned)mgrid), dim3(64), 0, stream, p);
   return check_launch("kf_attn_decode(merge)");
 }
 

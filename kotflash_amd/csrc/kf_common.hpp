@@ -60,6 +60,13 @@ template <> struct Elem<_Float16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
+  // v_mfma_f32_16x16x32_f16: A lane l holds row l % 16, B lane l column l % 16,
+  // both with the eight k slots of lane group l / 16; C lane l register r holds
+  // C[4 (l / 16) + r][l % 16].
+  __device__ static inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
   __device__ static inline uint16_t bits(float x) {
     return __builtin_bit_cast(uint16_t, (_Float16)x);
   }
@@ -72,6 +79,10 @@ template <> struct Elem<__bf16> {
   using v8 = bf16x8;
   __device__ static inline f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
   __device__ static inline uint16_t bits(float x) {
@@ -307,6 +318,19 @@ __device__ inline float wave_xor32_max(float x) {
 __device__ inline float wave_xor32_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Combine the four 16-lane groups of a wave (lanes i, i + 16, i + 32, i + 48):
+// v_permlane16_swap pairs groups (0, 1) and (2, 3) the same way
+// v_permlane32_swap pairs the two halves, so both steps leave every lane of
+// the four groups with the same, bit-identical result.
+__device__ inline float wave_group16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return wave_xor32_max(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+__device__ inline float wave_group16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return wave_xor32_sum(__uint_as_float(r[0]) + __uint_as_float(r[1]));
 }
 
 // Wave index inside the workgroup as a wave-uniform (scalar) value, so that
