@@ -23,6 +23,11 @@ One JSON line on stdout (everything else goes to stderr):
   fp16): microseconds per call (split-KV kernel + LSE merge) from HIP-graph
   replays of back-to-back calls over 32 rotating K/V sets (537 MB, larger than
   the 256 MB Infinity Cache), and HBM GB/s of the 16,781,376 algorithmic bytes.
+* ``configs``: the other BASELINE configurations timed on the GPU: config 1
+  (forward only), config 2 over Sk in {2048, 4096, 8192, 16384}, config 3 in
+  bf16, config 4 (non-causal MHA fwd+bwd, D = 72 and 96) and config 5 (64
+  steps of per-sequence KV append + ragged split-KV decode on a
+  [8, 8, 32768, 64] cache), each with its own roofline fraction.
 * ``cpu_baseline``: the reference's SDPA path (native-GQA
   scaled_dot_product_attention, fp32, autograd backward) on the host CPU at the
   full config 3 shape, median of 5 timed steps after one warm-up.
@@ -64,25 +69,25 @@ def seeded(torch, shape, seed, dtype, scale=1.0, device="cuda"):
     return (torch.randn(*shape, generator=g) * scale).to(dtype).to(device)
 
 
-def bench_train(torch, _hip, dtype, steps, warmup):
-    c = CFG3
+def bench_train(torch, _hip, dtype, steps, warmup, cfg=None, causal=True, qkv_scale=0.5):
+    c = cfg or CFG3
     b, hq, hkv, s, d = c["B"], c["Hq"], c["Hkv"], c["S"], c["D"]
     scale = 1.0 / math.sqrt(d)
-    q = seeded(torch, (b, hq, s, d), 301, dtype, 0.5)
-    k = seeded(torch, (b, hkv, s, d), 302, dtype, 0.5)
-    v = seeded(torch, (b, hkv, s, d), 303, dtype, 0.5)
+    q = seeded(torch, (b, hq, s, d), 301, dtype, qkv_scale)
+    k = seeded(torch, (b, hkv, s, d), 302, dtype, qkv_scale)
+    v = seeded(torch, (b, hkv, s, d), 303, dtype, qkv_scale)
     do = seeded(torch, (b, hq, s, d), 304, dtype)
     out = torch.empty_like(q)
     lse = torch.empty((b, hq, s), device=q.device, dtype=torch.float32)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    ws = torch.empty(_hip.bwd_workspace_bytes(b, hq, hkv, s, s, d, True), device=q.device,
+    ws = torch.empty(_hip.bwd_workspace_bytes(b, hq, hkv, s, s, d, causal), device=q.device,
                      dtype=torch.uint8)
 
     def fwd():
-        _hip.fwd(q, k, v, out, lse, causal=True, scale=scale)
+        _hip.fwd(q, k, v, out, lse, causal=causal, scale=scale)
 
     def bwd(stages):
-        _hip.bwd(q, k, v, out, lse, do, dq, dk, dv, causal=True, scale=scale,
+        _hip.bwd(q, k, v, out, lse, do, dq, dk, dv, causal=causal, scale=scale,
                  workspace=ws, stages=stages)
 
     def step(ev=None):
@@ -135,7 +140,7 @@ def bench_train(torch, _hip, dtype, steps, warmup):
         "bwd_dkdv": isolated(lambda: bwd(_hip.KF_BWD_DKDV)),
         "bwd_dkdv_fixup": isolated(lambda: bwd(_hip.KF_BWD_DKDV_FIXUP)),
     }
-    f = fwd_flops(b, hq, s, d)
+    f = fwd_flops(b, hq, s, d) if causal else 4.0 * d * b * hq * s * s
     work = {"attn_fwd": f, "bwd_dq": 0.5 * f, "bwd_dkdv": 2.0 * f, "bwd_dkdv_fixup": 0.0}
     return ms, wall_ms, dkdv_live, per, work, 3.5 * f
 
@@ -238,6 +243,147 @@ def bench_decode(torch, _hip, dtype, sk, replays=20):
                 timing="HIP graph replays of 32 back-to-back calls over 32 K/V sets (537 MB)")
 
 
+def bench_config5(torch, _hip, steps=64, seed=500):
+    """cache [8, 8, 32768, 64] fp16 with per-sequence
+    lengths U[4096, 28000] (seeded); each of `steps` steps appends n in
+    [1, 16] tokens per sequence at its own position (append kernel, device
+    int64 starts) and decodes Hq=32 query heads x n rows per sequence over its
+    visible prefix (split-KV decode with device int32 lengths). All inputs of
+    the 64 steps are staged on the GPU first; the 64 (append, decode) pairs are
+    captured in one HIP graph and one replay is timed between two events. Unused capacity
+    holds NaN, as in the parity test. Bytes per step: append
+    2 (K, V) x 2 (read + write) x B Hkv n D x 2; decode K + V of every visible
+    prefix + Q + O + LSE."""
+    b, hkv, cap, d, hq = 8, 8, 32768, 64, 32
+    g = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(4096, 28001, (b,), generator=g).tolist()
+    ns = [int(torch.randint(1, 17, (1,), generator=g)) for _ in range(steps)]
+    kc = torch.full((b, hkv, cap, d), float("nan"), dtype=torch.float16, device="cuda")
+    vc = torch.full_like(kc, float("nan"))
+    for i, n in enumerate(lengths):
+        kc[i, :, :n] = seeded(torch, (hkv, n, d), 510 + i, torch.float16)
+        vc[i, :, :n] = seeded(torch, (hkv, n, d), 520 + i, torch.float16)
+    plan = []
+    cur = list(lengths)
+    app_bytes = dec_bytes = 0
+    for t, n in enumerate(ns):
+        starts = torch.tensor(cur, dtype=torch.int64, device="cuda")
+        cur = [x + n for x in cur]
+        seqlens = torch.tensor(cur, dtype=torch.int32, device="cuda")
+        maxlen = max(cur)
+        nk = seeded(torch, (b, hkv, n, d), 600 + t, torch.float16)
+        nv = seeded(torch, (b, hkv, n, d), 700 + t, torch.float16)
+        q = seeded(torch, (b, hq, n, d), 800 + t, torch.float16)
+        out = torch.empty_like(q)
+        splits = _hip.decode_num_splits(b, hq, hkv, n, maxlen, d)
+        ws = torch.empty(max(256, _hip.decode_workspace_bytes(b, hq, hkv, n, d, splits)),
+                         dtype=torch.uint8, device="cuda")
+        plan.append((nk, nv, starts, seqlens, maxlen, q, out, splits, ws))
+        app_bytes += 2 * 2 * b * hkv * n * d * 2
+        dec_bytes += 2 * hkv * d * 2 * sum(cur) + 2 * b * hq * n * d * 2 + b * hq * n * 4
+    scale = 1.0 / math.sqrt(d)
+
+    def append(i):
+        nk, nv, starts = plan[i][0], plan[i][1], plan[i][2]
+        _hip.kv_append(kc, vc, nk, nv, start_dev=starts)
+
+    def decode(i):
+        _, _, _, seqlens, maxlen, q, out, splits, ws = plan[i]
+        _hip.decode(q, kc[:, :, :maxlen], vc[:, :, :maxlen], out, None, seqlens, scale=scale,
+                    num_splits=splits, workspace=ws)
+
+    def timed(fn):
+        # Captured into a HIP graph so the figure is GPU time, not the
+        # host's launch rate; replayed once to warm, then timed.
+        fn()
+        torch.cuda.synchronize()
+        stream = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            fn()
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=stream):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        z.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(z) * 1e3  # us
+
+    both = timed(lambda: [f(i) for i in range(steps) for f in (append, decode)])
+    app = timed(lambda: [append(i) for i in range(steps)])
+    dec = timed(lambda: [decode(i) for i in range(steps)])
+    if not all(bool(torch.isfinite(p[6]).all()) for p in plan):
+        raise RuntimeError("config 5: non-finite decode output")
+    return {"workload": "BASELINE config 5: cache [8,8,32768,64] fp16, lengths U[4096,28000], "
+                        f"{steps} steps of append n in [1,16] + ragged decode Hq=32",
+            "steps": steps, "tokens_appended": sum(ns), "us_total": both,
+            "us_per_step": both / steps,
+            "append": {"us_per_step": app / steps, "bytes": app_bytes,
+                       "hbm_gbps": app_bytes / (app * 1e-6) / 1e9,
+                       "hbm_frac": app_bytes / (app * 1e-6) / PEAK_HBM},
+            "decode": {"us_per_step": dec / steps, "bytes": dec_bytes,
+                       "hbm_gbps": dec_bytes / (dec * 1e-6) / 1e9,
+                       "hbm_frac": dec_bytes / (dec * 1e-6) / PEAK_HBM,
+                       "us_per_token": dec / sum(ns)},
+            "timing": "64 staged steps captured in one HIP graph, one replay between two HIP "
+                      "events (after a warm replay)"}
+
+
+def bench_forward_only(torch, _hip, cfg, causal, reps=50):
+    """Forward (O + LSE) alone, `reps` back-to-back launches between two events."""
+    b, hq, hkv, s, d = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["S"], cfg["D"]
+    q = seeded(torch, (b, hq, s, d), 101, torch.float16)
+    k = seeded(torch, (b, hkv, s, d), 102, torch.float16)
+    v = seeded(torch, (b, hkv, s, d), 103, torch.float16)
+    out = torch.empty_like(q)
+    lse = torch.empty((b, hq, s), device=q.device, dtype=torch.float32)
+    fn = lambda: _hip.fwd(q, k, v, out, lse, causal=causal, scale=1.0 / math.sqrt(d))
+    fn()
+    torch.cuda.synchronize()
+    a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    z.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(z) * 1e3 / reps
+    f = fwd_flops(b, hq, s, d) if causal else 4.0 * d * b * hq * s * s
+    return {"us_per_call": us, "tflops": f / (us * 1e-6) / 1e12,
+            "frac": f / (us * 1e-6) / PEAK_MFMA_F16}
+
+
+def side_configs(torch, _hip, steps):
+    """The other BASELINE configurations, each timed on the GPU."""
+    res = {}
+    c1 = dict(B=2, Hq=8, Hkv=2, S=512, D=64)
+    res["config1_forward"] = dict(
+        workload="BASELINE config 1 on the GPU: causal GQA forward B=2 Hq=8 Hkv=2 S=512 D=64 fp16",
+        **bench_forward_only(torch, _hip, c1, True))
+    res["config2_decode_sweep"] = {}
+    for sk in (2048, 4096, 8192, 16384):
+        r = bench_decode(torch, _hip, torch.float16, sk)
+        res["config2_decode_sweep"][str(sk)] = {k: r[k] for k in
+                                                ("us_per_call", "hbm_gbps", "hbm_frac", "num_splits")}
+    ms, _, _, per, work, flops = bench_train(torch, _hip, torch.bfloat16, steps, steps // 2)
+    res["config3_bf16"] = {"ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+                           "frac": flops / (ms * 1e-3) / PEAK_MFMA_F16}
+    for dd in (72, 96):
+        c4 = dict(B=4, Hq=12, Hkv=12, S=2048, D=dd)
+        ms, _, _, per, work, flops = bench_train(torch, _hip, torch.float16, steps, steps // 2, c4,
+                                                 causal=False, qkv_scale=1.0)
+        res[f"config4_d{dd}"] = {
+            "workload": f"BASELINE config 4: non-causal MHA fwd+bwd B=4 H=12 S=2048 D={dd} fp16",
+            "ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+            "frac": flops / (ms * 1e-3) / PEAK_MFMA_F16,
+            "flop_convention": "unpadded D: fwd 4 B H S^2 D, fwd+bwd 3.5x"}
+    res["config5_append_decode"] = bench_config5(torch, _hip)
+    return res
+
+
 def cpu_baseline(dtype_name):
     """The reference's SDPA path on host cores (fp32, native GQA, autograd
     backward), timed by the oracle's restatement of it at the config 3 shape."""
@@ -295,6 +441,8 @@ def main() -> int:
     ap.add_argument("--dtype", choices=("float16", "bfloat16"), default="float16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-side", action="store_true",
+                    help="skip the other BASELINE configurations (1, 2 sweep, 3 bf16, 4, 5)")
     ap.add_argument("--pmc-sample", action="store_true",
                     help="run one config 3 step plus a calibration fill/copy for rocprofv3 "
                          "--pmc and exit (prints no bench line)")
@@ -344,6 +492,9 @@ def main() -> int:
     decode = None if args.no_decode else bench_decode(torch, _hip, torch.float16, CFG2["Sk"])
     if decode:
         log(f"decode: {decode}")
+    side = None if args.no_side else side_configs(torch, _hip, max(20, args.steps // 4))
+    if side:
+        log(f"side configs: {json.dumps(side)}")
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.dtype)
     value = step_flops / (ms * 1e-3) / 1e12
     line = {
@@ -368,6 +519,7 @@ def main() -> int:
         "kernels": kernels,
         "roofline": roofline,
         "decode": decode,
+        "configs": side,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
