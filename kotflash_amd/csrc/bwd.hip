@@ -319,6 +319,9 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
       f32x16 s = zero16(), dp = zero16();
       static_for<0, LA>([&](auto mc) { read_op(decltype(mc)::value); });
       __builtin_amdgcn_sched_barrier(0);
+      // Raised priority while this wave issues MFMAs, so that the other wave
+      // on the SIMD runs its softmax in the gaps instead of competing for them.
+      __builtin_amdgcn_s_setprio(1);
       static_for<0, NSD>([&](auto mc) {
         constexpr int m = decltype(mc)::value;
         if constexpr (m & 1)
@@ -328,6 +331,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
         if constexpr (m + LA < NSD + NDQ) read_op(m + LA);
         __builtin_amdgcn_sched_barrier(0);
       });
+      __builtin_amdgcn_s_setprio(0);
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = fmaf(s[r], p.scale_log2, -lse2);
       if (need_mask) {
@@ -343,12 +347,14 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
       for (int r = 0; r < 16; ++r) dp[r] = fast_exp2(s[r]) * (dp[r] - dlt);
       const u32x4 ds0 = pack8<T>(dp, 0), ds1 = pack8<T>(dp, 8);
       __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
       static_for<0, NDQ>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
         dq[j >> 1] = Elem<T>::mfma(op[NSD + j], (j & 1) ? ds1 : ds0, dq[j >> 1]);
         if constexpr (NSD + j + LA < NSD + NDQ) read_op(NSD + j + LA);
         __builtin_amdgcn_sched_barrier(0);
       });
+      __builtin_amdgcn_s_setprio(0);
     }
     KF_WAIT_VMCNT(0);  // this wave's loads of the next tile
     __syncthreads();   // every wave's loads landed; stage ST is free again

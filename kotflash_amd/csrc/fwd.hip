@@ -226,6 +226,10 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
       }
       static_for<0, LA>([&](auto mc) { read_k(decltype(mc)::value); });
       __builtin_amdgcn_sched_barrier(0);
+      // Raised priority while this wave issues MFMAs (S here, PV below), so
+      // that the other wave on the SIMD runs its softmax in the gaps instead
+      // of competing for them.
+      __builtin_amdgcn_s_setprio(1);
       static_for<0, NS>([&](auto mc) {
         constexpr int m = decltype(mc)::value;
 #pragma unroll
@@ -236,6 +240,7 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
         __builtin_amdgcn_sched_barrier(0);
       });
 
+      __builtin_amdgcn_s_setprio(0);
       const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && kbase + BN - 1 > wq0);
       u32x4 pk[QB][4];
 #pragma unroll
@@ -297,6 +302,7 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
       }
 
       __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
       static_for<0, NPV>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
 #pragma unroll
@@ -305,6 +311,7 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
         if constexpr (j + LA < NPV) read_v(j + LA);
         __builtin_amdgcn_sched_barrier(0);
       });
+      __builtin_amdgcn_s_setprio(0);
     }
     KF_WAIT_VMCNT(0);  // this wave's loads of the next tile
     __syncthreads();   // every wave's loads landed; stage ST is free again
