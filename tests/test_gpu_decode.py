@@ -155,3 +155,39 @@ def test_ragged_decode_with_empty_splits_and_nan_tail():
     for i, n in enumerate(lengths):
         eo, _ = reference_fp32(q[i:i + 1], kc[i:i + 1, :, :n], vc[i:i + 1, :, :n], causal=False)
         assert_close(out[i:i + 1], eo, **FWD_TOL[F16], what=f"seq {i}")
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16])
+@pytest.mark.parametrize("hq,hkv,q_seq,d", [
+    (4, 1, 4, 64),    # 16 packed rows: one full 16-row block
+    (17, 1, 1, 64),   # 17 rows: a second block with a single row
+    (8, 1, 4, 128),   # 32 rows: two 16-row blocks
+    (11, 1, 3, 96),   # 33 rows: four-block workgroup, partly empty
+    (16, 1, 4, 64),   # 64 rows: four full blocks
+    (13, 1, 5, 72),   # 65 rows: a second row block; head dim padded to 96
+])
+def test_decode_row_block_edges(dtype, hq, hkv, q_seq, d):
+    """Packed-row counts (G * Sq) on both sides of the 16-row MFMA blocks and
+    of the 16/32/64-row workgroup tiles."""
+    q = seeded((2, hq, q_seq, d), 291, dtype=dtype)
+    k = seeded((2, hkv, 3000, d), 292, dtype=dtype)
+    v = seeded((2, hkv, 3000, d), 293, dtype=dtype)
+    with torch.no_grad():
+        out = attention(q, k, v, causal=False, backend="hip")
+    eo, _ = reference_fp32(q, k, v, causal=False)
+    assert_close(out, eo, **FWD_TOL[dtype], what="O")
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_decode_merge_many_splits(d):
+    """One KV group with a long cache: the planner picks 256 splits, more than
+    one merge lane reads in a single round trip, so the merge walks several
+    chunks with its running rescale."""
+    q = seeded((1, 4, 1, d), 295, dtype=F16)
+    k = seeded((1, 1, 65536, d), 296, dtype=F16)
+    v = seeded((1, 1, 65536, d), 297, dtype=F16)
+    assert _hip.decode_num_splits(1, 4, 1, 1, 65536, d) > 64
+    out, lse = attention_forward(q, k, v, causal=False, scale=1 / math.sqrt(d))
+    eo, el = reference_fp32(q, k, v, causal=False)
+    assert_close(out, eo, **FWD_TOL[F16], what="O")
+    assert_close(lse, el, **FWD_TOL[F16], what="LSE")
