@@ -248,7 +248,8 @@ def bench_config5(torch, _hip, steps=64, seed=500):
     lengths U[4096, 28000] (seeded); each of `steps` steps appends n in
     [1, 16] tokens per sequence at its own position (append kernel, device
     int64 starts) and decodes Hq=32 query heads x n rows per sequence over its
-    visible prefix (split-KV decode with device int32 lengths). All inputs of
+    visible prefix (split-KV decode with device int32 lengths, splits planned
+    from the host-side lengths by kf_decode_num_splits_ragged). All inputs of
     the 64 steps are staged on the GPU first; the 64 (append, decode) pairs are
     captured in one HIP graph and one replay is timed between two events. Unused capacity
     holds NaN, as in the parity test. Bytes per step: append
@@ -275,7 +276,7 @@ def bench_config5(torch, _hip, steps=64, seed=500):
         nv = seeded(torch, (b, hkv, n, d), 700 + t, torch.float16)
         q = seeded(torch, (b, hq, n, d), 800 + t, torch.float16)
         out = torch.empty_like(q)
-        splits = _hip.decode_num_splits(b, hq, hkv, n, maxlen, d)
+        splits = _hip.decode_num_splits_ragged(b, hq, hkv, n, cur, d)
         ws = torch.empty(max(256, _hip.decode_workspace_bytes(b, hq, hkv, n, d, splits)),
                          dtype=torch.uint8, device="cuda")
         plan.append((nk, nv, starts, seqlens, maxlen, q, out, splits, ws))

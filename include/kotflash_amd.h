@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define KF_ABI_VERSION 1
+#define KF_ABI_VERSION 2
 
 enum kf_status {
   KF_OK = 0,
@@ -115,6 +115,18 @@ int kf_attn_bwd_stages(int stages, const void* q, const void* k, const void* v, 
  * to whole granules) partitions Sk into exactly that many splits.
  */
 int kf_decode_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D);
+
+/*
+ * The same for a ragged batch whose visible lengths are known on the host
+ * (lengths: B entries; Sk of the kf_attn_decode call is max(lengths)). The
+ * chunk is sized from the total visible keys, so that the non-empty splits of
+ * short and long sequences fill the GPU evenly; splits beyond a sequence's
+ * length are empty and cheap. No reference counterpart: the reference's cache
+ * has one scalar length (kotflash/cache.py:122) and its planner one Sk
+ * (kotflash/_planning.py:25-34).
+ */
+int kf_decode_num_splits_ragged(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
+                                const int32_t* lengths, int64_t D);
 
 /* Workspace for kf_attn_decode in bytes (fp32 partial O and LSE per split);
  * 0 when num_splits == 1. */

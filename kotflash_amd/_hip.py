@@ -19,7 +19,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libkotflash_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 KF_F16, KF_BF16 = 0, 1
 KF_BWD_DELTA, KF_BWD_DQ, KF_BWD_DKDV, KF_BWD_DKDV_FIXUP = 1, 2, 4, 8
 KF_BWD_ALL = KF_BWD_DELTA | KF_BWD_DQ | KF_BWD_DKDV | KF_BWD_DKDV_FIXUP
@@ -44,6 +44,8 @@ _SIGNATURES = {
                                 _I64, _I64, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P, _I64P,
                                 _I64P, _F, _I, _I, _P, _SZ, _P]),
     "kf_decode_num_splits": (_I, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "kf_decode_num_splits_ragged": (_I, [_I64, _I64, _I64, _I64, ctypes.POINTER(ctypes.c_int32),
+                                         _I64]),
     "kf_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I]),
     "kf_attn_decode": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                             _I64P, _I64P, _I64P, _I64P, _F, _I, _I, _P, _SZ, _P]),
@@ -162,6 +164,12 @@ def bwd(q, k, v, out, lse, dout, dq, dk, dv, *, causal: bool, scale: float,
 
 def decode_num_splits(b, hq, hkv, sq, sk, d) -> int:
     return int(lib().kf_decode_num_splits(b, hq, hkv, sq, sk, d))
+
+
+def decode_num_splits_ragged(b, hq, hkv, sq, lengths, d) -> int:
+    """Split count for a ragged batch from its host-side visible lengths."""
+    lens = (ctypes.c_int32 * len(lengths))(*[int(x) for x in lengths])
+    return int(lib().kf_decode_num_splits_ragged(b, hq, hkv, sq, lens, d))
 
 
 def decode_workspace_bytes(b, hq, hkv, sq, d, num_splits) -> int:

@@ -309,7 +309,7 @@ class RaggedKVCache(PreallocatedKVCache):
 
             return attention_decode_ragged(
                 q, self.k, self.v, self.seqlens, max_seqlen=max(self.lengths),
-                scale=1.0 / (q.shape[-1] ** 0.5),
+                scale=1.0 / (q.shape[-1] ** 0.5), host_lengths=self.lengths,
             )
         outs = []
         for b in range(q.shape[0]):

@@ -104,6 +104,19 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   const int c1 = min(c0 + p.chunk, L);
   // This wave's steps: 32-key blocks c0 + 32 (wave + 4 j), j = 0 .. nst - 1.
   const int nst = c1 > c0 + 32 * wave ? cdiv(c1 - c0 - 32 * wave, 128) : 0;
+  const int nrow = min(RB, R - rb * RB);
+  const int grp = (b * p.Hkv + kvh) * p.nrb + rb;
+  const int64_t pbase = ((int64_t)grp * p.nsplit + split) * RB;
+  if (c1 <= c0 && p.nsplit > 1) {
+    // A split past this sequence's visible length (ragged batches): weight 0
+    // in the merge, written without loading anything.
+    for (int e = tid; e < nrow * (p.D / 4); e += 256) {
+      const int r = e / (p.D / 4), d = (e % (p.D / 4)) * 4;
+      *reinterpret_cast<float4*>(p.part_o + (pbase + r) * p.D + d) = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (d == 0) p.part_lse[pbase + r] = kNegInf;
+    }
+    return;
+  }
 
   // K/V resources end at the chunk's last visible key: keys at or beyond c1
   // (the range check includes the scalar offset) load as zeros.
@@ -301,7 +314,6 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   float* obuf = reinterpret_cast<float*>(smem);  // [4][RB][OSTR]
   float* mbuf = obuf + 4 * RB * OSTR;            // [4][RB]
   float* lbuf = mbuf + 4 * RB;                   // [4][RB]
-  const int nrow = min(RB, R - rb * RB);
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     if (qb * 16 >= nrow) break;
@@ -321,8 +333,6 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
 
   // Output: final O/LSE (one split) or this split's fp32 partial.
   const int DQ = p.D / 4;
-  const int grp = (b * p.Hkv + kvh) * p.nrb + rb;
-  const int64_t pbase = ((int64_t)grp * p.nsplit + split) * RB;
   for (int e = tid; e < nrow * DQ; e += 256) {
     const int r = e / DQ, d = (e % DQ) * 4;
     float M = kNegInf;
@@ -512,9 +522,37 @@ extern "C" int kf_decode_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t 
   return (int)ns;
 }
 
+// Ragged batches: workgroups the planner aims for (about four per CU), so
+// that short sequences' splits and long ones' even out across the CUs.
+constexpr int64_t kDecRaggedWGs = 1024;
+
 static int64_t decode_row_blocks(int64_t G, int64_t Sq) {
   const int rb = decode_rows_per_wg(G, Sq);
   return (G * Sq + rb - 1) / rb;
+}
+
+extern "C" int kf_decode_num_splits_ragged(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
+                                           const int32_t* lengths, int64_t D) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Sq <= 0 || D <= 0 || Hq % Hkv || lengths == nullptr) return 1;
+  int64_t maxlen = 0, total = 0;
+  for (int64_t b = 0; b < B; ++b) {
+    const int64_t L = lengths[b] > 0 ? lengths[b] : 0;
+    maxlen = L > maxlen ? L : maxlen;
+    total += L;
+  }
+  if (maxlen <= 0) return 1;
+  // Chunk from the total visible work: the non-empty splits of all sequences
+  // add up to about kDecRaggedWGs workgroups. Splits past a sequence's length
+  // are empty and end at once.
+  const int64_t stage = kDecGranule;
+  const int64_t units = Hkv * decode_row_blocks(Hq / Hkv, Sq);
+  int64_t chunk = (units * total + kDecRaggedWGs - 1) / kDecRaggedWGs;
+  chunk = (chunk < stage ? stage : chunk + stage - 1) / stage * stage;
+  int64_t ns = (maxlen + chunk - 1) / chunk;
+  // Normalise the way kf_attn_decode derives the chunk from the count.
+  chunk = ((maxlen + ns - 1) / ns + stage - 1) / stage * stage;
+  ns = (maxlen + chunk - 1) / chunk;
+  return (int)ns;
 }
 
 extern "C" size_t kf_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,

@@ -9,7 +9,7 @@ masked).
 """
 from __future__ import annotations
 
-from typing import Optional
+from typing import Optional, Sequence
 
 import torch
 
@@ -45,12 +45,16 @@ def strided_decode_supported(q, k, v) -> bool:
     return _hip.is_gfx950(q.device) and _hip.library_available()
 
 
-def _decode(q, k, v, seqlens: Optional[torch.Tensor], scale: float, with_lse: bool):
+def _decode(q, k, v, seqlens: Optional[torch.Tensor], scale: float, with_lse: bool,
+            host_lengths: Optional[Sequence[int]] = None):
     b, hq, sq, d = q.shape
     hkv, sk = k.shape[1], k.shape[2]
     out = torch.empty((b, hq, sq, d), device=q.device, dtype=q.dtype)
     lse = torch.empty((b, hq, sq), device=q.device, dtype=torch.float32) if with_lse else None
-    splits = _hip.decode_num_splits(b, hq, hkv, sq, sk, d)
+    if host_lengths is not None and max(host_lengths) == sk:
+        splits = _hip.decode_num_splits_ragged(b, hq, hkv, sq, host_lengths, d)
+    else:
+        splits = _hip.decode_num_splits(b, hq, hkv, sq, sk, d)
     nbytes = _hip.decode_workspace_bytes(b, hq, hkv, sq, d, splits)
     ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8) if nbytes else None
     _hip.decode(q, k, v, out, lse, seqlens, scale=scale, num_splits=splits, workspace=ws)
@@ -104,11 +108,14 @@ def attention_forward_strided_append(q, k_cache, v_cache, new_k, new_v, *,
 
 
 def attention_decode_ragged(q, k_cache, v_cache, seqlens: torch.Tensor, *, max_seqlen: int,
-                            scale: float, with_lse: bool = False):
+                            scale: float, with_lse: bool = False,
+                            host_lengths: Optional[Sequence[int]] = None):
     """Non-causal decode where batch entry b sees cache positions
     [0, seqlens[b]). ``seqlens`` is a device int32 [B] tensor and
-    ``max_seqlen`` >= max(seqlens) bounds the planned splits. Returns O, or
-    (O, LSE) with ``with_lse``."""
+    ``max_seqlen`` >= max(seqlens) bounds the planned splits. ``host_lengths``
+    (the same lengths on the host, with max == max_seqlen) lets the planner
+    size the splits from the total visible work. Returns O, or (O, LSE) with
+    ``with_lse``."""
     require_hip_tensors("ragged decode", q, k_cache, v_cache)
     if seqlens.dtype != torch.int32 or seqlens.device != q.device or seqlens.shape != (q.shape[0],):
         raise ValueError("seqlens must be a device int32 tensor of shape [B]")
@@ -125,5 +132,8 @@ def attention_decode_ragged(q, k_cache, v_cache, seqlens: torch.Tensor, *, max_s
     v_view = v_cache[:, :, :max_seqlen]
     if not all(_hip.layout_ok(t) for t in (q, k_view, v_view)):
         raise ValueError("ragged decode needs inner-contiguous, 16-byte aligned tensors")
-    out, lse = _decode(q, k_view, v_view, seqlens, float(scale), with_lse=with_lse)
+    if host_lengths is not None and len(host_lengths) != q.shape[0]:
+        raise ValueError("host_lengths must have one entry per batch element")
+    out, lse = _decode(q, k_view, v_view, seqlens, float(scale), with_lse=with_lse,
+                       host_lengths=host_lengths)
     return (out, lse) if with_lse else out

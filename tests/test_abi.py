@@ -110,3 +110,27 @@ def test_append_argument_validation():
     assert rc == 1 and "capacity" in lib.kf_last_error().decode()
     rc = lib.kf_kv_append(None, 0x2000, 0x3000, 0x4000, None, 0, 1, 1, 3, 8, 64, s3, s3, s4, s4, 0, None)
     assert rc == 1 and "null" in lib.kf_last_error().decode()
+
+
+def test_ragged_decode_planner():
+    """The ragged planner's count partitions max(lengths) into whole 128-key
+    granules, sizes the chunk from the total visible keys (about 1024
+    non-empty workgroups), and degrades to one split for empty batches."""
+    lib = _hip.lib()
+
+    def plan(lengths, b=None, hq=32, hkv=8, sq=1, d=64):
+        return _hip.decode_num_splits_ragged(b or len(lengths), hq, hkv, sq, lengths, d)
+
+    for lengths in ([4096, 28000, 129, 7777], [1, 1, 1], [16384] * 2, [65536], [300, 20000]):
+        ns = plan(lengths)
+        mx = max(lengths)
+        chunk = ((-(-mx // ns)) + 127) // 128 * 128
+        assert ns >= 1 and -(-mx // chunk) == ns
+    # Config 5 shape: total visible keys x kv heads / 1024 workgroups.
+    lengths = [4096, 28000, 16000, 9000, 22000, 5000, 12000, 27000]
+    ns = plan(lengths)
+    chunk = ((-(-28000 // ns)) + 127) // 128 * 128
+    nonempty = sum(8 * -(-x // chunk) for x in lengths)
+    assert 700 <= nonempty <= 1400
+    assert plan([0, 0]) == 1
+    assert lib.kf_decode_num_splits_ragged(2, 8, 2, 1, None, 64) == 1
