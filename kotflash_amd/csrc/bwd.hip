@@ -421,6 +421,33 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
 
   f32x16 dk[NDB], dv[NDB];
 
+  // LDS read bases (bytes): stage 0 and, because a ds_read immediate is only
+  // 16 bits, stage 2. Row reads of the Q / dO A operands: lane row l32,
+  // logical chunk 2 ks + h32. Transposed reads: the lo / hi rows
+  // 4 h + p / 4 (+ 8) of a 16-row block at head-dim block db. The other
+  // stage, the dO tile and other row blocks are whole multiples of 16 rows
+  // away, which keep the swizzle key, so they are immediate offsets.
+  constexpr uint32_t kStageBytes = 2u * QT * 2u;
+  uint32_t rdq[NKS], rdq2[NKS], trb[NDB][2], trb2[NDB][2];
+  {
+    const uint32_t s0 = lds_addr(&stage[0][0][0]);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      rdq[ks] = s0 + (uint32_t)Tile::chunk(l32, 2 * ks + h32) * 16u;
+      rdq2[ks] = rdq[ks] + 2u * kStageBytes;
+    }
+    const int pl = lane & 15, g = (lane >> 4) & 1;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi) {
+        const int r = 4 * h32 + (pl >> 2) + 8 * hi;
+        const int col = 32 * db + 16 * g + 4 * (pl & 3);
+        trb[db][hi] = s0 + (uint32_t)Tile::elem(r, col) * 2u;
+        trb2[db][hi] = trb[db][hi] + 2u * kStageBytes;
+      }
+  }
+
   int kt = 0;
   int64_t row_base = 0;  // first unit of key-tile row kt
   bool first_seg = true;
@@ -492,7 +519,6 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
     // LDS byte addresses (M0) of stage 0's blocks for this wave.
     const uint32_t lds_q0 = lds_addr(&stage[0][0][0]) + (uint32_t)(wave * NQI) * 1024u;
     const uint32_t lds_s0 = lds_addr(&rowstat[0][0][0]) + (uint32_t)wave * (kBMQ * 4u);
-    constexpr uint32_t kStageBytes = 2u * QT * 2u;
     constexpr uint32_t kStatBytes = 4u * kBMQ * 4u;
     // Units are walked in order (query head g, query tile qt): `Walk`
     // advances one unit without divisions.
@@ -565,9 +591,8 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
     // short window keeps few operand registers live) and, spread over the
     // middle slots, the DMA of unit + 2. The MFMAs run on the matrix core
     // while the interleaved VALU, LDS and memory instructions issue.
-    auto unit = [&](int st, int qrow0, const Dma& nd) {
-      const uint16_t* Qs = stage[st][0];
-      const uint16_t* Ds = stage[st][1];
+    auto unit = [&](auto stc, int qrow0, const Dma& nd) {
+      constexpr int st = decltype(stc)::value;
       constexpr int NSD = 2 * NKS;  // S/dP MFMAs per block
       constexpr int NVK = 4 * NDB;  // dV/dK MFMAs per block
       constexpr int NSLOT = 2 * NSD + 2 * NVK;
@@ -577,16 +602,22 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
       f32x4 l4[2][4], d4[2][4];
       u32x4 pk[2][4];               // P lo/hi, dS lo/hi
 
-      // Slot m -> (kind, block, index): kind 0 = S/dP, 1 = dV/dK.
+      // Slot m -> (kind, block, index): kind 0 = S/dP, 1 = dV/dK. Every read
+      // is a per-lane base register plus an immediate (stage, tile, row block).
       auto read_op = [&](int m) {
+        constexpr uint32_t kStage = (st == 2 ? 0u : (uint32_t)st * kStageBytes);
         if (m < 2 * NSD) {
           const int qb = m / NSD, i = m % NSD, ks = i >> 1;
-          op[m] = lds_read16(((i & 1) ? Ds : Qs) + Tile::chunk(qb * 32 + l32, 2 * ks + h32) * 8);
+          const uint32_t off = kStage + ((i & 1) ? QT * 2u : 0u) + (uint32_t)(qb * 32 * CPR * 16);
+          op[m] = *(const KF_LDS u32x4*)(uintptr_t)((st == 2 ? rdq2[ks] : rdq[ks]) + off);
         } else {
           const int qb = (m - 2 * NSD) / NVK, j = (m - 2 * NSD) % NVK;
           const int db = j % NDB, w = j / NDB;  // w: dV lo, dK lo, dV hi, dK hi
           const bool isv = (w & 1) == 0;
-          op[m] = lds_read_tr_operand_sw<CPR>(isv ? Ds : Qs, qb * 32 + 16 * (w >> 1), 32 * db, lane);
+          const uint32_t off = kStage + (isv ? QT * 2u : 0u) + (uint32_t)((qb * 32 + 16 * (w >> 1)) * CPR * 16);
+          const u32x2 lo = lds_read_tr16_at((st == 2 ? trb2[db][0] : trb[db][0]) + off);
+          const u32x2 hi = lds_read_tr16_at((st == 2 ? trb2[db][1] : trb[db][1]) + off);
+          op[m] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
       };
       auto mfma_slot = [&](int m) {
@@ -617,17 +648,15 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
       };
       // S layout: lane = key, register r = query row 8 (r/4) + 4 h + r % 4.
       // Causal mask of block qb: key <= row  <=>  t <= 8 (r/4) + r % 4 with
-      // t = key - (block row 0) - 4 h; blocks clear of the diagonal get a t
-      // that passes every comparison (branch-free: one body for all units;
-      // two specialised bodies exceed the register budget).
-      int t[2];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-        t[qb] = CAUSAL && qrow0 + 32 * qb < kw0 + 31 ? key - (qrow0 + 32 * qb) - 4 * h32 : -(1 << 30);
+      // t = key - (block row 0) - 4 h. It is folded into the row statistics:
+      // a masked (row, key) element gets LSE = +inf in this lane's copy, so
+      // exp2(scale S - LSE) = 0 there and the softmax itself has no mask
+      // instructions. Only blocks that cross this wave's diagonal take the
+      // (wave-uniform) branch that does it; one unit body serves all units
+      // (two specialised bodies exceed the register budget).
       auto soft = [&](int qb, int r) {
         const int g4 = r >> 2, e = r & 3;
-        float x = fmaf(s[qb][r], p.scale_log2, -l4[qb][g4][e]);
-        if (CAUSAL) x = t[qb] <= 8 * g4 + e ? x : kNegInf;
+        const float x = fmaf(s[qb][r], p.scale_log2, -l4[qb][g4][e]);
         const float pv = fast_exp2(x);
         s[qb][r] = pv;
         dp[qb][r] = pv * dp[qb][r];  // dP accumulated from -delta: dS = P (dP - delta)
@@ -646,6 +675,14 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
       // first MFMA.
       auto init_block = [&](int qb) {
         read_stats(qb);
+        if (CAUSAL && qrow0 + 32 * qb < kw0 + 31) {
+          const int t = key - (qrow0 + 32 * qb) - 4 * h32;
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              l4[qb][g4][e] = t <= 8 * g4 + e ? l4[qb][g4][e] : __builtin_inff();
+        }
         s[qb] = zero16();
 #pragma unroll
         for (int r = 0; r < 16; ++r) dp[qb][r] = d4[qb][r >> 2][r & 3];
@@ -706,19 +743,25 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
       for (int j = 0; j < NDMA; ++j) dma_issue(d1, j);
       walk_next(wdma);
     }
-    int st = 0;
-    for (int it = ua; it < ub; ++it) {
-      KF_WAIT_VMCNT(NDMA);  // unit it + 1's loads may still be in flight
-      __syncthreads();
-      const Dma nd = dma_setup(wdma, st == 0 ? NST - 1 : st - 1, it + 2 < ub);
-      // Rows >= Sq and keys >= Sk need no mask: their Q/dO (K/V) rows load as
-      // zeros and their LSE/delta as 0, so they add nothing to any valid dK/dV
-      // row. A unit entirely above the causal diagonal for this wave is
-      // computed fully masked rather than branched around.
-      unit(st, wcur.qt * kBMQ, nd);
-      walk_next(wcur);
-      walk_next(wdma);
-      st = st == NST - 1 ? 0 : st + 1;
+    // The loop is unrolled by the ring's NST stages, so that every LDS offset
+    // inside a unit is a compile-time constant.
+    for (int it0 = ua; it0 < ub; it0 += NST) {
+      static_for<0, NST>([&](auto stc) {
+        constexpr int st = decltype(stc)::value;
+        const int it = it0 + st;
+        if (it < ub) {
+          KF_WAIT_VMCNT(NDMA);  // unit it + 1's loads may still be in flight
+          __syncthreads();
+          const Dma nd = dma_setup(wdma, st == 0 ? NST - 1 : st - 1, it + 2 < ub);
+          // Rows >= Sq and keys >= Sk need no mask: their Q/dO (K/V) rows load
+          // as zeros and their LSE/delta as 0, so they add nothing to any valid
+          // dK/dV row. A unit entirely above the causal diagonal for this wave
+          // is computed fully masked rather than branched around.
+          unit(stc, wcur.qt * kBMQ, nd);
+          walk_next(wcur);
+          walk_next(wdma);
+        }
+      });
     }
 
     // Flush: dK^T / dV^T layout is lane = key, register r = head_dim
