@@ -654,18 +654,30 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
       // instructions. Only blocks that cross this wave's diagonal take the
       // (wave-uniform) branch that does it; one unit body serves all units
       // (two specialised bodies exceed the register budget).
-      auto soft = [&](int qb, int r) {
+      // The softmax of an element runs in three stages spread over three
+      // consecutive slots (exponent argument, exp2, then dS = P dP and the
+      // packing of every eighth element), so the VALU instructions of a slot
+      // belong to different elements and do not wait on each other: with one
+      // wave per SIMD, a dependent chain inside a slot holds back the next
+      // slot's MFMA.
+      float xs[2][16], pv[2][16], dsv[2][16];
+      auto soft_a = [&](int qb, int r) {
         const int g4 = r >> 2, e = r & 3;
-        const float x = fmaf(s[qb][r], p.scale_log2, -l4[qb][g4][e]);
-        const float pv = fast_exp2(x);
-        s[qb][r] = pv;
-        dp[qb][r] = pv * dp[qb][r];  // dP accumulated from -delta: dS = P (dP - delta)
-        if (r == 7) {
-          pk[qb][0] = pack8<T>(s[qb], 0);
-          pk[qb][2] = pack8<T>(dp[qb], 0);
-        } else if (r == 15) {
-          pk[qb][1] = pack8<T>(s[qb], 8);
-          pk[qb][3] = pack8<T>(dp[qb], 8);
+        xs[qb][r] = fmaf(s[qb][r], p.scale_log2, -l4[qb][g4][e]);
+      };
+      auto soft_b = [&](int qb, int r) { pv[qb][r] = fast_exp2(xs[qb][r]); };
+      auto soft_c = [&](int qb, int r) {
+        dsv[qb][r] = pv[qb][r] * dp[qb][r];  // dP accumulated from -delta: dS = P (dP - delta)
+        if ((r & 7) == 7) {
+          const int h = r >> 3, r0 = r - 7;
+          u32x4 a, d;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            a[i] = pack2<T>(pv[qb][r0 + 2 * i], pv[qb][r0 + 2 * i + 1]);
+            d[i] = pack2<T>(dsv[qb][r0 + 2 * i], dsv[qb][r0 + 2 * i + 1]);
+          }
+          pk[qb][h] = a;
+          pk[qb][2 + h] = d;
         }
       };
 
@@ -710,18 +722,24 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
         mfma_slot(m);
         if constexpr (m + LA < NSLOT) read_op(m + LA);
         if constexpr (m == NSD - 3) init_block(1);
-        if constexpr (m >= NSD && m < 2 * NSD) {
-          static_for<0, EPS0>([&](auto ec) {
-            constexpr int r = (m - NSD) * EPS0 + decltype(ec)::value;
-            if constexpr (r < 16) soft(0, r);
+        // Softmax stages of block qb whose window starts at slot S: slot m
+        // runs stage a of its own elements, stage b of the previous slot's
+        // and stage c of the one before.
+        auto soft_slot = [&](auto qbc, auto sc, auto epsc) {
+          constexpr int qb = decltype(qbc)::value, S = decltype(sc)::value;
+          constexpr int EPS = decltype(epsc)::value;
+          static_for<0, EPS>([&](auto ec) {
+            constexpr int e = decltype(ec)::value;
+            constexpr int ra = (m - S) * EPS + e, rb = (m - S - 1) * EPS + e, rc = (m - S - 2) * EPS + e;
+            if constexpr (m >= S + 2 && rc >= 0 && rc < 16) soft_c(qb, rc);
+            if constexpr (m >= S + 1 && rb >= 0 && rb < 16) soft_b(qb, rb);
+            if constexpr (m >= S && ra < 16) soft_a(qb, ra);
           });
-        }
-        if constexpr (m >= 2 * NSD && m < 2 * NSD + NVK) {
-          static_for<0, EPS1>([&](auto ec) {
-            constexpr int r = (m - 2 * NSD) * EPS1 + decltype(ec)::value;
-            if constexpr (r < 16) soft(1, r);
-          });
-        }
+        };
+        soft_slot(std::integral_constant<int, 0>{}, std::integral_constant<int, NSD>{},
+                  std::integral_constant<int, EPS0>{});
+        soft_slot(std::integral_constant<int, 1>{}, std::integral_constant<int, 2 * NSD>{},
+                  std::integral_constant<int, EPS1>{});
         if constexpr (m >= DMA0 && (m - DMA0) % DMAS == 0 && (m - DMA0) / DMAS < NDMA)
           dma_issue(nd, (m - DMA0) / DMAS);
         __builtin_amdgcn_sched_barrier(0);
