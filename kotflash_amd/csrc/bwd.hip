@@ -102,36 +102,50 @@ __device__ inline int dkdv_owner(const DkdvSplit& sp, int nwg, int64_t u) {
 }
 
 // ---------------------------------------------------------------------------
-// 1. delta = rowsum(O * dO): 16 lanes per row, 16 rows per workgroup.
+// 1. delta = rowsum(O * dO): 16 lanes per row (one 16-byte chunk of each
+// matrix per lane and row), 64 rows per workgroup; every lane issues the loads
+// of its four rows before using any, so a workgroup costs one memory round
+// trip.
+constexpr int kDeltaRows = 64;
 template <typename T>
 __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
   const int tid = threadIdx.x;
   const int rsub = tid >> 4, c16 = tid & 15;
   const int64_t total = (int64_t)p.B * p.Hq * p.Sq;
-  const int64_t row = (int64_t)blockIdx.x * 16 + rsub;
-  float acc = 0.f;
-  if (row < total) {
-    const int64_t bh = row / p.Sq;
-    const int i = (int)(row - bh * p.Sq);
-    const int b = (int)(bh / p.Hq), h = (int)(bh % p.Hq);
-    const uint16_t* Op = p.o + b * p.o_sb + h * p.o_sh + i * p.o_ss;
-    const uint16_t* Dp = p.dout + b * p.do_sb + h * p.do_sh + i * p.do_ss;
-    for (int c = c16; c * 8 < p.D; c += 16) {
-      const u32x4 a = ldg16(Op + c * 8), g = ldg16(Dp + c * 8);
+  constexpr int RPT = kDeltaRows / 16;  // rows per 16-lane group
+  u32x4 a[RPT], g[RPT];
+  int64_t rows[RPT];
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        acc += Elem<T>::to_f32((uint16_t)(a[w] & 0xffff)) * Elem<T>::to_f32((uint16_t)(g[w] & 0xffff));
-        acc += Elem<T>::to_f32((uint16_t)(a[w] >> 16)) * Elem<T>::to_f32((uint16_t)(g[w] >> 16));
-      }
-    }
+  for (int j = 0; j < RPT; ++j) {
+    const int64_t row = (int64_t)blockIdx.x * kDeltaRows + j * 16 + rsub;
+    rows[j] = row;
+    const int64_t rr = row < total ? row : 0;
+    const int64_t bh = rr / p.Sq;
+    const int i = (int)(rr - bh * p.Sq);
+    const int b = (int)(bh / p.Hq), h = (int)(bh % p.Hq);
+    const auto orr = make_rsrc(p.o + b * p.o_sb + h * p.o_sh + i * p.o_ss, (uint32_t)p.D * 2u);
+    const auto drr = make_rsrc(p.dout + b * p.do_sb + h * p.do_sh + i * p.do_ss, (uint32_t)p.D * 2u);
+    // D <= 128: 16 lanes cover a row's 16-byte chunks.
+    const uint32_t off = row < total && c16 * 8 < p.D ? (uint32_t)c16 * 16u : kOOB;
+    a[j] = buf_load16(orr, off);
+    g[j] = buf_load16(drr, off);
   }
-  acc += __shfl_xor(acc, 8);
-  acc += __shfl_xor(acc, 4);
-  acc += __shfl_xor(acc, 2);
-  acc += __shfl_xor(acc, 1);
-  if (c16 == 0 && row < total) {
-    p.delta[row] = -acc;
-    p.lse2[row] = p.lse[row] * kLog2e;
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      acc += Elem<T>::to_f32((uint16_t)(a[j][w] & 0xffff)) * Elem<T>::to_f32((uint16_t)(g[j][w] & 0xffff));
+      acc += Elem<T>::to_f32((uint16_t)(a[j][w] >> 16)) * Elem<T>::to_f32((uint16_t)(g[j][w] >> 16));
+    }
+    acc += __shfl_xor(acc, 8);
+    acc += __shfl_xor(acc, 4);
+    acc += __shfl_xor(acc, 2);
+    acc += __shfl_xor(acc, 1);
+    if (c16 == 0 && rows[j] < total) {
+      p.delta[rows[j]] = -acc;
+      p.lse2[rows[j]] = p.lse[rows[j]] * kLog2e;
+    }
   }
 }
 
@@ -956,7 +970,7 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
   // when the dK/dV stage runs without it.
   if ((stages & KF_BWD_DELTA) && !(stages & KF_BWD_DQ)) {
     const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
-    hipLaunchKernelGGL((delta_kernel<T>), dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((delta_kernel<T>), dim3((unsigned)((rows + kDeltaRows - 1) / kDeltaRows)), dim3(256), 0, stream, p);
     int rc = check_launch("kf_attn_bwd(delta)");
     if (rc) return rc;
   }

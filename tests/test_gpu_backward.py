@@ -171,3 +171,25 @@ def test_bf16_gradients_no_worse_than_torch(shape):
         ea = float((a.float() - e).abs().max())
         et = float((t.float() - e).abs().max())
         assert ea <= 1.25 * et + 2e-3, f"d{n}: ours {ea:.4f} vs torch {et:.4f}"
+
+
+def test_backward_stages_called_separately():
+    """The stage mask of kf_attn_bwd_stages: the row deltas from the delta
+    kernel (the dK/dV stage run without dQ in the same call), then dQ, dK/dV
+    and the fixup as separate calls, agree with fp32 autograd."""
+    from kotflash_amd import _hip
+    q = seeded((2, 4, 300, 64), 91, dtype=F16, scale=0.5)
+    k = seeded((2, 2, 300, 64), 92, dtype=F16, scale=0.5)
+    v = seeded((2, 2, 300, 64), 93, dtype=F16, scale=0.5)
+    do = seeded((2, 4, 300, 64), 94, dtype=F16)
+    out, lse = attention_forward(q, k, v, causal=True, scale=0.125)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = torch.empty(_hip.bwd_workspace_bytes(2, 4, 2, 300, 300, 64, True), device="cuda",
+                     dtype=torch.uint8)
+    for st in (_hip.KF_BWD_DELTA, _hip.KF_BWD_DKDV, _hip.KF_BWD_DKDV_FIXUP, _hip.KF_BWD_DQ):
+        _hip.bwd(q, k, v, out, lse, do, dq, dk, dv, causal=True, scale=0.125, workspace=ws,
+                 stages=st)
+    _, _, (eq, ek, ev) = reference_fp32(q, k, v, causal=True, with_grad_out=do)
+    assert_close(dq, eq, **BWD_TOL[F16], what="dQ")
+    assert_close(dk, ek, **BWD_TOL[F16], what="dK")
+    assert_close(dv, ev, **BWD_TOL[F16], what="dV")
