@@ -181,25 +181,12 @@ def _blockwise_backward(q, k, v, out, lse, grad_out, *, causal: bool, scale: flo
     return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype)
 
 
-class _HipAttention(torch.autograd.Function):
-    """Autograd op over the HIP forward/backward; saves (q, k, v, out, lse) as
-    the reference's custom op does (kotflash/attention.py:203-220)."""
+def _hip_op_attention(q, k, v, causal: bool, scale: float) -> torch.Tensor:
+    """O through the ``kotflash_amd::attn_fwd`` custom op, whose registered
+    backward is ``kotflash_amd::attn_bwd`` (so torch.compile traces it)."""
+    from .ops import attn_fwd
 
-    @staticmethod
-    def forward(ctx, q, k, v, causal: bool, scale: float):
-        out, lse = attention_forward(q, k, v, causal=causal, scale=scale)
-        ctx.save_for_backward(q, k, v, out, lse)
-        ctx.causal = causal
-        ctx.scale = scale
-        return out
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        q, k, v, out, lse = ctx.saved_tensors
-        dq, dk, dv = attention_backward(
-            q, k, v, out, lse, grad_out, causal=ctx.causal, scale=ctx.scale
-        )
-        return dq, dk, dv, None, None
+    return attn_fwd(q, k, v, causal, scale)[0]
 
 
 def hip_supported(q: torch.Tensor, k: torch.Tensor) -> bool:
@@ -269,11 +256,11 @@ def attention(
                 "HIP backend requires an AMD MI355X (gfx950) GPU with the kotflash_amd "
                 "library built, FP16 or BF16 and 8 <= head_dim <= 128"
             )
-        return _HipAttention.apply(q, k, v, causal, float(scale))
+        return _hip_op_attention(q, k, v, causal, float(scale))
 
     if backend == "auto":
         if route == "hip":
-            return _HipAttention.apply(q, k, v, causal, float(scale))
+            return _hip_op_attention(q, k, v, causal, float(scale))
         profile = _t4_profile_backend(q, k, v, causal=causal, scale=float(scale))
         if profile == "sdpa_expanded":
             return _sdpa_expanded(q, k, v, causal=causal, scale=scale)
