@@ -88,11 +88,23 @@ def device_arch(index: int) -> str:
     return torch.cuda.get_device_properties(index).gcnArchName.split(":")[0]
 
 
+_GFX950_BY_INDEX: dict = {}
+
+
 def is_gfx950(device: torch.device) -> bool:
-    if device.type != "cuda" or not torch.cuda.is_available():
+    if device.type != "cuda":
         return False
-    index = device.index if device.index is not None else torch.cuda.current_device()
-    return device_arch(index) == "gfx950"
+    index = device.index
+    hit = _GFX950_BY_INDEX.get(index)
+    if hit is not None:
+        return hit
+    if not torch.cuda.is_available():
+        return False
+    dev_index = index if index is not None else torch.cuda.current_device()
+    result = device_arch(dev_index) == "gfx950"
+    if index is not None:
+        _GFX950_BY_INDEX[index] = result  # explicit indices never change meaning
+    return result
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -103,9 +115,13 @@ def dtype_code(dtype: torch.dtype) -> int:
     raise TypeError(f"HIP kernels support float16 and bfloat16, got {dtype}")
 
 
-def _strides(t: torch.Tensor, n: int = 3):
-    arr = (ctypes.c_int64 * 4)(*t.stride())
-    return ctypes.cast(arr, _I64P), arr  # keep arr alive with the pointer
+_I64x4 = ctypes.c_int64 * 4
+
+
+def _strides(t: torch.Tensor):
+    """The tensor's strides as a ctypes int64[4] (passed where the C ABI
+    takes ``const int64_t*``; ctypes hands over the array's address)."""
+    return _I64x4(*t.stride())
 
 
 def _check(rc: int, what: str) -> None:
@@ -114,8 +130,39 @@ def _check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed (code {rc}): {msg}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device: torch.device) -> int:
+    """PyTorch's current HIP stream on ``device``, as a raw handle."""
+    if _raw_stream is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(index)
     return torch.cuda.current_stream(device).cuda_stream
+
+
+class _DeviceGuard:
+    """Makes ``device`` current for a launch; free when it already is (the
+    usual case), unlike torch.cuda.device's unconditional exchange."""
+
+    __slots__ = ("index", "prev")
+
+    def __init__(self, device: torch.device):
+        self.index = device.index if device.index is not None else -1
+        self.prev = -1
+
+    def __enter__(self):
+        if self.index >= 0:
+            cur = torch.cuda.current_device()
+            if cur != self.index:
+                self.prev = cur
+                torch.cuda.set_device(self.index)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev >= 0:
+            torch.cuda.set_device(self.prev)
+        return False
 
 
 def layout_ok(t: torch.Tensor) -> bool:
@@ -132,15 +179,16 @@ def fwd(q, k, v, out, lse, *, causal: bool, scale: float) -> None:
     b, hq, sq, d = q.shape
     _, hkv, sk, _ = k.shape
     keep = [_strides(t) for t in (q, k, v, out)]
-    with torch.cuda.device(q.device):
+    with _DeviceGuard(q.device):
         rc = lib().kf_attn_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
-            b, hq, hkv, sq, sk, d, *(s[0] for s in keep),
+            b, hq, hkv, sq, sk, d, *keep,
             float(scale), int(bool(causal)), dtype_code(q.dtype), _stream(q.device),
         )
     _check(rc, "kf_attn_fwd")
 
 
+@lru_cache(maxsize=256)
 def bwd_workspace_bytes(b, hq, hkv, sq, sk, d, causal) -> int:
     return int(lib().kf_attn_bwd_workspace_bytes(b, hq, hkv, sq, sk, d, int(bool(causal))))
 
@@ -150,11 +198,11 @@ def bwd(q, k, v, out, lse, dout, dq, dk, dv, *, causal: bool, scale: float,
     b, hq, sq, d = q.shape
     _, hkv, sk, _ = k.shape
     keep = [_strides(t) for t in (q, k, v, out, dout, dq, dk, dv)]
-    with torch.cuda.device(q.device):
+    with _DeviceGuard(q.device):
         rc = lib().kf_attn_bwd_stages(
             int(stages), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
             dout.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-            b, hq, hkv, sq, sk, d, *(s[0] for s in keep),
+            b, hq, hkv, sq, sk, d, *keep,
             float(scale), int(bool(causal)), dtype_code(q.dtype),
             workspace.data_ptr(), workspace.numel() * workspace.element_size(),
             _stream(q.device),
@@ -162,6 +210,7 @@ def bwd(q, k, v, out, lse, dout, dq, dk, dv, *, causal: bool, scale: float,
     _check(rc, "kf_attn_bwd")
 
 
+@lru_cache(maxsize=256)
 def decode_num_splits(b, hq, hkv, sq, sk, d) -> int:
     return int(lib().kf_decode_num_splits(b, hq, hkv, sq, sk, d))
 
@@ -172,6 +221,7 @@ def decode_num_splits_ragged(b, hq, hkv, sq, lengths, d) -> int:
     return int(lib().kf_decode_num_splits_ragged(b, hq, hkv, sq, lens, d))
 
 
+@lru_cache(maxsize=256)
 def decode_workspace_bytes(b, hq, hkv, sq, d, num_splits) -> int:
     return int(lib().kf_decode_workspace_bytes(b, hq, hkv, sq, d, num_splits))
 
@@ -183,12 +233,12 @@ def decode(q, k, v, out, lse: Optional[torch.Tensor], seqlens: Optional[torch.Te
     keep = [_strides(t) for t in (q, k, v, out)]
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    with torch.cuda.device(q.device):
+    with _DeviceGuard(q.device):
         rc = lib().kf_attn_decode(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
             lse.data_ptr() if lse is not None else None,
             seqlens.data_ptr() if seqlens is not None else None,
-            b, hq, hkv, sq, sk, d, *(s[0] for s in keep),
+            b, hq, hkv, sq, sk, d, *keep,
             float(scale), int(num_splits), dtype_code(q.dtype), ws_ptr, ws_bytes,
             _stream(q.device),
         )
@@ -199,11 +249,11 @@ def kv_append(k_cache, v_cache, new_k, new_v, *, start: int = 0,
               start_dev: Optional[torch.Tensor] = None) -> None:
     b, h, s, d = new_k.shape
     keep = [_strides(t) for t in (k_cache, v_cache, new_k, new_v)]
-    with torch.cuda.device(k_cache.device):
+    with _DeviceGuard(k_cache.device):
         rc = lib().kf_kv_append(
             k_cache.data_ptr(), v_cache.data_ptr(), new_k.data_ptr(), new_v.data_ptr(),
             start_dev.data_ptr() if start_dev is not None else None, int(start),
-            b, h, s, d, k_cache.shape[2], *(x[0] for x in keep),
+            b, h, s, d, k_cache.shape[2], *keep,
             dtype_code(k_cache.dtype), _stream(k_cache.device),
         )
     _check(rc, "kf_kv_append")

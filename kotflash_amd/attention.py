@@ -24,6 +24,7 @@ from .kernels.hip_decode import attention_forward_strided_decode, strided_decode
 from .kernels.hip_forward import attention_forward, triton_turing_supported
 
 BACKENDS = ("auto", "hip", "triton", "sdpa")
+_DTYPE_NAMES = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float32"}
 
 
 def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
@@ -135,8 +136,7 @@ def _gfx950_profile_backend(q, k, v, *, causal: bool):
     if not q.is_cuda or not _hip.is_gfx950(q.device):
         return None
     route = gfx950_profile_for_shapes(
-        tuple(q.shape), tuple(k.shape), causal=causal,
-        dtype_name=str(q.dtype).replace("torch.", ""),
+        q.shape, k.shape, causal=causal, dtype_name=_DTYPE_NAMES.get(q.dtype, ""),
     )
     if route == "hip" and not _hip.library_available():
         # A gfx950 device without the library is a broken install, not an
@@ -183,7 +183,14 @@ def _blockwise_backward(q, k, v, out, lse, grad_out, *, causal: bool, scale: flo
 
 def _hip_op_attention(q, k, v, causal: bool, scale: float) -> torch.Tensor:
     """O through the ``kotflash_amd::attn_fwd`` custom op, whose registered
-    backward is ``kotflash_amd::attn_bwd`` (so torch.compile traces it)."""
+    backward is ``kotflash_amd::attn_bwd`` (so torch.compile traces it).
+    Eager calls that need no gradient launch the forward directly, without
+    the op's dispatch (about 7 us of host time per call)."""
+    if not torch.compiler.is_compiling() and not (
+        torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
+    ):
+        out = attention_forward(q, k, v, causal=causal, scale=scale)[0]
+        return out if out.is_contiguous() else out.contiguous()
     from .ops import attn_fwd
 
     return attn_fwd(q, k, v, causal, scale)[0]
