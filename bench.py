@@ -382,7 +382,53 @@ def side_configs(torch, _hip, steps):
             "frac": flops / (ms * 1e-3) / PEAK_MFMA_F16,
             "flop_convention": "unpadded D: fwd 4 B H S^2 D, fwd+bwd 3.5x"}
     res["config5_append_decode"] = bench_config5(torch, _hip)
+    res["torch_sdpa_same_gpu"] = bench_sdpa_comparison(torch)
     return res
+
+
+def bench_sdpa_comparison(torch, steps=20, warmup=5):
+    """PyTorch's own GPU SDPA (the reference's fallback path, attention.py:126)
+    against the HIP kernels on the same MI355X, both through the public
+    ``attention`` API with identical synthetic inputs and HIP-event timing
+    over back-to-back calls: config 3 fwd+bwd, config 1 forward, config 2
+    decode at Sk=16384."""
+    import kotflash_amd as kf
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    cases = (
+        ("config3_fwd_bwd_us", CFG3, True, True, 0.5),
+        ("config1_fwd_us", dict(B=2, Hq=8, Hkv=2, S=512, D=64), True, False, 1.0),
+        ("config2_decode_sk16384_us", dict(B=2, Hq=8, Hkv=2, S=1, Sk=16384, D=64), False, False, 1.0),
+    )
+    out = {"timing": "HIP events over back-to-back public-API calls (host overhead included)"}
+    for name, c, causal, bwd, sc in cases:
+        sk = c.get("Sk", c["S"])
+        q = seeded(torch, (c["B"], c["Hq"], c["S"], c["D"]), 901, torch.float16, sc).requires_grad_(bwd)
+        k = seeded(torch, (c["B"], c["Hkv"], sk, c["D"]), 902, torch.float16, sc).requires_grad_(bwd)
+        v = seeded(torch, (c["B"], c["Hkv"], sk, c["D"]), 903, torch.float16, sc).requires_grad_(bwd)
+        do = seeded(torch, (c["B"], c["Hq"], c["S"], c["D"]), 904, torch.float16)
+        row = {}
+        for backend in ("hip", "sdpa"):
+            def call(backend=backend):
+                o = kf.attention(q, k, v, causal=causal, backend=backend)
+                if bwd:
+                    torch.autograd.grad(o, (q, k, v), do)
+            row[backend] = timed(call)
+        row["speedup"] = row["sdpa"] / row["hip"]
+        out[name] = row
+    return out
 
 
 def cpu_baseline(dtype_name):
