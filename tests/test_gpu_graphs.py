@@ -1,0 +1,114 @@
+"""HIP-graph capture of the launch paths: each graph is replayed several
+times with new inputs written eagerly between replays (and synchronizations),
+and every replay is checked against an eager run on the same inputs. The
+kernels are deterministic, so replays must match bit for bit."""
+import pytest
+import torch
+
+import kotflash_amd as kf
+from kotflash_amd import _hip
+from tests.gpu_helpers import seeded
+
+pytestmark = pytest.mark.gpu
+F16 = torch.float16
+
+
+def _capture(fn):
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fn()  # warm-up outside the graph (plans, allocator pools)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            result = fn()
+    torch.cuda.synchronize()
+    return graph, result
+
+
+def test_public_decode_graph_replays():
+    q = seeded((2, 8, 1, 64), 1201, dtype=F16)
+    k = seeded((2, 2, 4096, 64), 1202, dtype=F16)
+    v = seeded((2, 2, 4096, 64), 1203, dtype=F16)
+    graph, out = _capture(lambda: kf.attention(q, k, v, causal=False, backend="hip"))
+    for r in range(3):
+        q.copy_(seeded(q.shape, 1300 + r, dtype=F16))
+        k.copy_(seeded(k.shape, 1310 + r, dtype=F16))
+        v.copy_(seeded(v.shape, 1320 + r, dtype=F16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        expected = kf.attention(q, k, v, causal=False, backend="hip")
+        assert torch.equal(out, expected), f"replay {r}"
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_forward_backward_graph_replays(causal):
+    b, hq, hkv, s, d = 1, 8, 2, 700, 128
+    q, k, v, do = (torch.empty(sh, dtype=F16, device="cuda") for sh in
+                   ((b, hq, s, d), (b, hkv, s, d), (b, hkv, s, d), (b, hq, s, d)))
+    out = torch.empty_like(q)
+    lse = torch.empty((b, hq, s), dtype=torch.float32, device="cuda")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = torch.empty(_hip.bwd_workspace_bytes(b, hq, hkv, s, s, d, causal), dtype=torch.uint8,
+                     device="cuda")
+
+    def step():
+        _hip.fwd(q, k, v, out, lse, causal=causal, scale=0.09)
+        _hip.bwd(q, k, v, out, lse, do, dq, dk, dv, causal=causal, scale=0.09, workspace=ws)
+
+    for t, seed in zip((q, k, v, do), (1401, 1402, 1403, 1404)):
+        t.copy_(seeded(t.shape, seed, dtype=F16))
+    graph, _ = _capture(step)
+    for r in range(3):
+        for t, seed in zip((q, k, v, do), (1500, 1510, 1520, 1530)):
+            t.copy_(seeded(t.shape, seed + r, dtype=F16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [x.clone() for x in (out, lse, dq, dk, dv)]
+        step()  # eager on the same inputs
+        torch.cuda.synchronize()
+        for name, g, e in zip(("O", "LSE", "dQ", "dK", "dV"), got, (out, lse, dq, dk, dv)):
+            assert torch.equal(g, e), f"replay {r}: {name}"
+
+
+def test_ragged_append_and_decode_graph_replays():
+    b, hkv, hq, cap, d, n = 3, 2, 8, 4096, 64, 2
+    lengths = [1500, 3000, 2200]
+    kc = torch.full((b, hkv, cap, d), float("nan"), dtype=F16, device="cuda")
+    vc = torch.full_like(kc, float("nan"))
+    for i, L in enumerate(lengths):
+        kc[i, :, :L] = seeded((hkv, L, d), 1600 + i, dtype=F16)
+        vc[i, :, :L] = seeded((hkv, L, d), 1610 + i, dtype=F16)
+    starts = torch.tensor(lengths, dtype=torch.int64, device="cuda")
+    seqlens = torch.tensor([L + n for L in lengths], dtype=torch.int32, device="cuda")
+    maxlen = max(lengths) + n
+    nk = torch.empty((b, hkv, n, d), dtype=F16, device="cuda")
+    nv = torch.empty_like(nk)
+    q = torch.empty((b, hq, n, d), dtype=F16, device="cuda")
+    out = torch.empty_like(q)
+    splits = _hip.decode_num_splits_ragged(b, hq, hkv, n, [L + n for L in lengths], d)
+    ws = torch.empty(max(256, _hip.decode_workspace_bytes(b, hq, hkv, n, d, splits)),
+                     dtype=torch.uint8, device="cuda")
+
+    def step():
+        _hip.kv_append(kc, vc, nk, nv, start_dev=starts)
+        _hip.decode(q, kc[:, :, :maxlen], vc[:, :, :maxlen], out, None, seqlens, scale=0.125,
+                    num_splits=splits, workspace=ws)
+
+    for t, seed in zip((nk, nv, q), (1701, 1702, 1703)):
+        t.copy_(seeded(t.shape, seed, dtype=F16))
+    graph, _ = _capture(step)
+    for r in range(3):
+        for t, seed in zip((nk, nv, q), (1800, 1810, 1820)):
+            t.copy_(seeded(t.shape, seed + r, dtype=F16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        step()
+        torch.cuda.synchronize()
+        assert torch.equal(got, out), f"replay {r}: O"
+        for i, L in enumerate(lengths):
+            assert torch.equal(kc[i, :, L:L + n], nk[i]) and torch.equal(vc[i, :, L:L + n], nv[i])
+        assert bool(torch.isfinite(out).all())
