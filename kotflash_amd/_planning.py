@@ -106,13 +106,40 @@ def gfx950_decode_eligible(sq: int, sk: int, d: int, *, causal: bool) -> bool:
             and gfx950_head_dim_ok(d))
 
 
+# Below this much forward work (FLOP) an eager call is bound by host time, and
+# PyTorch's SDPA, whose launch path is C++, finishes first. Measured on MI355X
+# through the public API (python -m kotflash_amd.benchmark, B=2 Hq=8 Hkv=2
+# D=64 causal, fp16; fwd / fwd+bwd us, HIP vs SDPA):
+#   S=256: 29.6/253 vs 27.3/188;  S=512: 29.8/243 vs 26.5/185;
+#   S=1024: 30.6/248 vs 36.6/263;  S=2048: 30.2/261 vs 57.5/411;
+#   and B=1 H=8 S=512 D=128 non-causal (1.1e9 FLOP): 32.3/250 vs 23.9/175.
+# Split-KV decode shapes are not subject to it (HIP decode is 14x faster at
+# config 2).
+GFX950_HIP_MIN_FWD_FLOPS = 1.5e9
+
+
+def attention_fwd_flops(q_shape: Sequence[int], k_shape: Sequence[int], *, causal: bool) -> float:
+    """4 D B Hq times the visible (query, key) pairs, upper-left causal."""
+    b, hq, sq, d = q_shape
+    sk = k_shape[2]
+    if causal:
+        full = max(0, sq - sk)          # rows that see every key
+        part = min(sq, sk)              # rows i < sk see i + 1 keys
+        pairs = part * (part + 1) // 2 + full * sk
+    else:
+        pairs = sq * sk
+    return 4.0 * d * b * hq * pairs
+
+
 def gfx950_profile_for_shapes(
     q_shape: Sequence[int], k_shape: Sequence[int], *, causal: bool, dtype_name: str,
 ) -> Optional[str]:
     """Backend chosen by ``backend="auto"`` on gfx950, else None (SDPA).
 
     The HIP kernels cover fp16/bf16 with 8 <= head_dim <= 128 for any
-    sequence lengths and GQA grouping; everything else goes to SDPA.
+    sequence lengths and GQA grouping. ``auto`` takes them for split-KV decode
+    shapes and for problems of at least ``GFX950_HIP_MIN_FWD_FLOPS``; smaller
+    ones, and everything outside that envelope, go to SDPA.
     """
     if dtype_name not in ("float16", "bfloat16"):
         return None
@@ -122,5 +149,9 @@ def gfx950_profile_for_shapes(
     if not gfx950_head_dim_ok(d) or k_shape[3] != d:
         return None
     if q_shape[1] % k_shape[1] != 0:
+        return None
+    if gfx950_decode_eligible(q_shape[2], k_shape[2], d, causal=causal):
+        return "hip"
+    if attention_fwd_flops(q_shape, k_shape, causal=causal) < GFX950_HIP_MIN_FWD_FLOPS:
         return None
     return "hip"

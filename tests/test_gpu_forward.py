@@ -139,12 +139,38 @@ def test_forward_is_deterministic():
 
 @pytest.mark.parametrize("dtype", [F16, BF16])
 def test_public_attention_routes_to_hip(dtype):
-    q = seeded((2, 8, 300, 64), 61, dtype=dtype)
-    k = seeded((2, 2, 300, 64), 62, dtype=dtype)
-    v = seeded((2, 2, 300, 64), 63, dtype=dtype)
+    """Large enough for ``auto`` to take the HIP kernels (>= 1.5e9 FLOP)."""
+    q = seeded((2, 8, 1100, 64), 61, dtype=dtype)
+    k = seeded((2, 2, 1100, 64), 62, dtype=dtype)
+    v = seeded((2, 2, 1100, 64), 63, dtype=dtype)
     for backend in ("auto", "hip", "triton"):
         out = attention(q, k, v, causal=True, backend=backend)
         eo, _ = reference_fp32(q, k, v, causal=True)
         assert_close(out, eo, **FWD_TOL[dtype], what=backend)
     maps = open("/proc/self/maps").read()
     assert "libkotflash_amd.so" in maps
+
+
+def test_auto_routing_by_problem_size(monkeypatch):
+    """``auto`` sends host-bound small problems to SDPA and the rest (and
+    split-KV decode) to the HIP kernels."""
+    import sys
+
+    api = sys.modules["kotflash_amd.attention"]  # the package attribute is the function
+    calls = []
+    real = api._sdpa
+
+    def counting_sdpa(*args, **kwargs):
+        calls.append(args[0].shape)
+        return real(*args, **kwargs)
+
+    monkeypatch.setattr(api, "_sdpa", counting_sdpa)
+    small = [seeded((2, 8 if i == 0 else 2, 512, 64), 70 + i, dtype=F16) for i in range(3)]
+    big = [seeded((2, 8 if i == 0 else 2, 1024, 64), 80 + i, dtype=F16) for i in range(3)]
+    dec = [seeded((2, 8 if i == 0 else 2, 1 if i == 0 else 2048, 64), 90 + i, dtype=F16)
+           for i in range(3)]
+    attention(*small, causal=True)
+    assert len(calls) == 1
+    attention(*big, causal=True)
+    attention(*dec, causal=False)
+    assert len(calls) == 1

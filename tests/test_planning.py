@@ -3,7 +3,7 @@ tests/test_planning.py:17-85, plus the gfx950 envelope)."""
 import pytest
 
 from kotflash_amd._planning import (
-    INT32_MAX, cdiv, check_int32_indexing, gfx950_decode_eligible,
+    INT32_MAX, attention_fwd_flops, cdiv, check_int32_indexing, gfx950_decode_eligible,
     gfx950_profile_for_shapes, split_kv_plan, t4_profile_for_shapes,
 )
 
@@ -98,4 +98,19 @@ def test_gfx950_envelope():
     assert gfx950_decode_eligible(16, 1024, 128, causal=False)
     assert not gfx950_decode_eligible(17, 16384, 64, causal=False)
     assert not gfx950_decode_eligible(1, 1023, 64, causal=False)
+
+
+def test_gfx950_auto_routing_by_size():
+    """auto keeps host-bound small problems on SDPA, takes the HIP kernels
+    from about 1.5e9 forward FLOP up, and always for split-KV decode."""
+    f16 = dict(dtype_name="float16")
+    # Config 1: 4 * 64 * 16 * 131328 (the survey's algorithmic work figure).
+    assert attention_fwd_flops((2, 8, 512, 64), (2, 2, 512, 64), causal=True) == 537919488
+    assert gfx950_profile_for_shapes((2, 8, 512, 64), (2, 2, 512, 64), causal=True, **f16) is None
+    assert gfx950_profile_for_shapes((2, 8, 1024, 64), (2, 2, 1024, 64), causal=True, **f16) == "hip"
+    assert gfx950_profile_for_shapes((1, 8, 512, 128), (1, 8, 512, 128), causal=False, **f16) is None
+    assert gfx950_profile_for_shapes((2, 8, 1, 64), (2, 2, 2048, 64), causal=False, **f16) == "hip"
+    # Causal pair count: Sq < Sk (upper-left) and Sq > Sk (late rows see all keys).
+    assert attention_fwd_flops((1, 1, 3, 8), (1, 1, 5, 8), causal=True) == 4 * 8 * (1 + 2 + 3)
+    assert attention_fwd_flops((1, 1, 5, 8), (1, 1, 3, 8), causal=True) == 4 * 8 * (1 + 2 + 3 + 3 + 3)
     assert not gfx950_decode_eligible(1, 16384, 64, causal=True)
