@@ -17,11 +17,13 @@
 //      tile the kernel recomputes S = Q K^T and dP = dO V^T and accumulates
 //      dV^T += dO^T P and dK^T += Q^T dS in registers, so the group sum over
 //      query heads happens in registers (reference :94-195, group loop
-//      :136-137, products :183-184). Work is split stream-K style: the (key tile, head, query tile)
-//      units of all tiles are laid end to end and every workgroup takes an
-//      equal share, so causal tiles of very different sizes still keep every
-//      CU busy until the end. A tile shared by several workgroups is written
-//      as fp32 partials and
+//      :136-137, products :183-184). Work is split stream-K style: the
+//      (KV group, key tile, head, query tile) units of all tiles are laid end
+//      to end and every workgroup takes an equal share, so causal tiles of
+//      very different sizes still keep every CU busy until the end; the
+//      shares of one XCD are consecutive, so its CUs stream the same KV
+//      group's Q/dO rows through one L2. A tile shared by several workgroups
+//      is written as fp32 partials and
 //   4. dkdv_fixup_kernel sums those partials (and zero-fills keys that no query
 //      can see); the reference instead splits long query ranges into a fixed
 //      number of fp32 partial copies plus a reduction pass (:198-332).
@@ -64,7 +66,7 @@ struct BwdParams {
   int G, ngroups;
   int nqt, nkt;    // dq: 128-row query tiles; dkdv: 64-row query tiles, 128-key tiles
   int nwg;         // dkdv workgroups (stream-K share count)
-  int64_t units;   // dkdv: total (key tile, head, query tile) units
+  int64_t units;   // dkdv: total (KV group, key tile, head, query tile) units
   float scale, scale_log2;
 };
 
@@ -91,7 +93,16 @@ constexpr int kMaxDkdvWG = 512;
 struct DkdvSplit {
   int start[kMaxDkdvWG + 1];
 };
-// The workgroup that owns unit u (start[] is non-decreasing, start[0] = 0).
+// Units are ordered (KV group, key tile, query head, query tile), and the
+// shares are laid out so that XCD x (the dispatcher sends workgroup i to XCD
+// i % 8) runs shares [x nwg / 8, (x + 1) nwg / 8): one XCD's CUs then work on
+// the same KV group(s), whose Q/dO rows they all stream, and share its L2.
+__device__ inline int dkdv_share_of_block(int block, int nwg) {
+  return (nwg & 7) == 0 ? (block & 7) * (nwg >> 3) + (block >> 3) : block;
+}
+
+// The share (stream-K range) that owns unit u (start[] is non-decreasing,
+// start[0] = 0).
 __device__ inline int dkdv_owner(const DkdvSplit& sp, int nwg, int64_t u) {
   int lo = 0, hi = nwg - 1;
   while (lo < hi) {
@@ -397,7 +408,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// 3. dK/dV, key-stationary, stream-K over (key tile, head, query tile) units.
+// 3. dK/dV, key-stationary, stream-K over (KV group, key tile, head, query
+// tile) units.
 // Four waves, one per SIMD (the 512-register budget lets the dK/dV
 // accumulators live in accumulation registers). Wave w owns keys
 // 32 w .. 32 w + 31 of the 128-key tile and keeps their K and V rows in
@@ -429,8 +441,9 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
   const int lane = tid & 63, wave = wave_index();
   const int l32 = lane & 31, h32 = lane >> 5;
 
-  int64_t u = sp.start[blockIdx.x];
-  const int64_t uend = sp.start[blockIdx.x + 1];
+  const int share = dkdv_share_of_block(blockIdx.x, p.nwg);
+  int64_t u = sp.start[share];
+  const int64_t uend = sp.start[share + 1];
   if (u >= uend) return;
 
   f32x16 dk[NDB], dv[NDB];
@@ -462,22 +475,25 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
       }
   }
 
+  const int64_t group_units = p.units / p.ngroups;
+  int grp = (int)(u / group_units);
   int kt = 0;
-  int64_t row_base = 0;  // first unit of key-tile row kt
+  int64_t row_base = grp * group_units;  // first unit of tile row (grp, kt)
   bool first_seg = true;
   while (u < uend) {
     for (;;) {
-      const int64_t row_units = (int64_t)p.ngroups * p.G * dkdv_nq(kt, p.nqt, CAUSAL);
+      const int64_t row_units = (int64_t)p.G * dkdv_nq(kt, p.nqt, CAUSAL);
       if (u < row_base + row_units) break;
       row_base += row_units;
-      ++kt;
+      if (++kt == p.nkt) {
+        kt = 0;
+        ++grp;
+      }
     }
     const int nq = dkdv_nq(kt, p.nqt, CAUSAL);
     const int qs = dkdv_qstart(kt, CAUSAL);
     const int per_tile = p.G * nq;
-    const int64_t off = u - row_base;
-    const int grp = (int)(off / per_tile);
-    const int ua = (int)(off % per_tile);
+    const int ua = (int)(u - row_base);
     const int ub = (int)min((int64_t)per_tile, ua + (uend - u));
     const int b = grp / p.Hkv, kvh = grp % p.Hkv;
     const int k0 = kt * kBNK;
@@ -534,20 +550,21 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
     const uint32_t lds_q0 = lds_addr(&stage[0][0][0]) + (uint32_t)(wave * NQI) * 1024u;
     const uint32_t lds_s0 = lds_addr(&rowstat[0][0][0]) + (uint32_t)wave * (kBMQ * 4u);
     constexpr uint32_t kStatBytes = 4u * kBMQ * 4u;
-    // Units are walked in order (query head g, query tile qt): `Walk`
-    // advances one unit without divisions.
+    // Units are walked in order (query head g, query tile qt descending):
+    // workgroups that start a tile row together read the same Q/dO tiles at
+    // the same time. `Walk` advances one unit without divisions.
     struct Walk {
       int g, qt;
     };
     auto walk_init = [&](int it) {
       Walk w;
       w.g = it / nq;
-      w.qt = qs + (it - w.g * nq);
+      w.qt = qs + nq - 1 - (it - w.g * nq);
       return w;
     };
     auto walk_next = [&](Walk& w) {
-      if (++w.qt == qs + nq) {
-        w.qt = qs;
+      if (--w.qt < qs) {
+        w.qt = qs + nq - 1;
         ++w.g;
       }
     };
@@ -800,7 +817,7 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
     // 32 db + 8 (r/4) + 4 h + r % 4. A tile this workgroup covered alone is
     // final; a shared one goes to this workgroup's partial slot.
     const bool full = ua == 0 && ub == per_tile;
-    float* slot = p.part + (int64_t)(2 * blockIdx.x + (first_seg ? 0 : 1)) * 2 * kBNK * DT;
+    float* slot = p.part + (int64_t)(2 * share + (first_seg ? 0 : 1)) * 2 * kBNK * DT;
     uint16_t* Dk = p.dk + b * p.dk_sb + kvh * p.dk_sh + key * p.dk_ss;
     uint16_t* Dv = p.dv + b * p.dv_sb + kvh * p.dv_sh + key * p.dv_ss;
 #pragma unroll
@@ -859,9 +876,8 @@ __global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p, cons
     }
     return;
   }
-  int64_t base = 0;
-  for (int k = 0; k < kt; ++k) base += (int64_t)p.ngroups * p.G * dkdv_nq(k, p.nqt, CAUSAL);
-  const int64_t first = base + (int64_t)grp * p.G * nq;
+  int64_t first = (int64_t)grp * (p.units / p.ngroups);
+  for (int k = 0; k < kt; ++k) first += (int64_t)p.G * dkdv_nq(k, p.nqt, CAUSAL);
   const int64_t last = first + (int64_t)p.G * nq - 1;
   const int w0 = dkdv_owner(sp, p.nwg, first), w1 = dkdv_owner(sp, p.nwg, last);
   if (w0 == w1) return;
@@ -936,10 +952,11 @@ static void dkdv_split(DkdvSplit& sp, int ngroups, int G, int nqt, int nkt, bool
     int w = 1;
     int64_t base = 0, cost = 0;
     cached.start[0] = 0;
-    for (int kt = 0; kt < nkt && w < nwg; ++kt) {
-      const int64_t units = (int64_t)G * dkdv_nq(kt, nqt, causal);
-      if (!units) continue;
-      for (int g = 0; g < ngroups && w < nwg; ++g) {
+    // Tile rows in unit order: KV group outer, key tile inner.
+    for (int g = 0; g < ngroups && w < nwg; ++g) {
+      for (int kt = 0; kt < nkt && w < nwg; ++kt) {
+        const int64_t units = (int64_t)G * dkdv_nq(kt, nqt, causal);
+        if (!units) continue;
         const int64_t row_cost = 8 * units + kSegmentCost8;
         // Boundaries whose target cost falls inside this tile row.
         while (w < nwg) {
