@@ -80,6 +80,8 @@ def test_backward_reference_cases(hq, hkv, sq, sk, d, causal, dtype):
 
 
 @pytest.mark.parametrize("shape", [
+    (3, 6, 3, 1000, 1000, 64, True),   # 9 KV groups: stream-K shares cross group boundaries
+    (3, 6, 3, 1000, 1000, 64, False),
     (1, 2, 1, 500, 130, 64, True),   # Sq > Sk causal: keys seen by many rows
     (1, 2, 2, 70, 900, 128, True),   # keys beyond Sq never seen: zero dK/dV
     (2, 3, 1, 129, 131, 40, False),  # head_dim 40, ragged tiles
