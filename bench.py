@@ -252,7 +252,10 @@ def bench_config5(torch, _hip, steps=64, seed=500):
     from the host-side lengths by kf_decode_num_splits_ragged). All inputs of
     the 64 steps are staged on the GPU first; the 64 (append, decode) pairs are
     captured in one HIP graph and one replay is timed between two events. Unused capacity
-    holds NaN, as in the parity test. Bytes per step: append
+    holds NaN, as in the parity test. The same 64 steps are also timed through
+    the fused entry (kf_attn_append_decode: the decode launch stores the new
+    tokens, no append launch) and its outputs checked against the two-launch
+    path's. Bytes per step: append
     2 (K, V) x 2 (read + write) x B Hkv n D x 2; decode K + V of every visible
     prefix + Q + O + LSE."""
     b, hkv, cap, d, hq = 8, 8, 32768, 64, 32
@@ -279,7 +282,15 @@ def bench_config5(torch, _hip, steps=64, seed=500):
         splits = _hip.decode_num_splits_ragged(b, hq, hkv, n, cur, d)
         ws = torch.empty(max(256, _hip.decode_workspace_bytes(b, hq, hkv, n, d, splits)),
                          dtype=torch.uint8, device="cuda")
-        plan.append((nk, nv, starts, seqlens, maxlen, q, out, splits, ws))
+        # Fused append + decode: splits over the old keys plus one for the
+        # new tokens, positions = the old lengths.
+        old = [x - n for x in cur]
+        fsplits = _hip.decode_num_splits_ragged(b, hq, hkv, n, old, d)
+        fws = torch.empty(_hip.decode_workspace_bytes(b, hq, hkv, n, d, fsplits + 1),
+                          dtype=torch.uint8, device="cuda")
+        fused = (torch.tensor(old, dtype=torch.int32, device="cuda"), max(old), fsplits, fws,
+                 torch.empty_like(q))
+        plan.append((nk, nv, starts, seqlens, maxlen, q, out, splits, ws, fused))
         app_bytes += 2 * 2 * b * hkv * n * d * 2
         dec_bytes += 2 * hkv * d * 2 * sum(cur) + 2 * b * hq * n * d * 2 + b * hq * n * 4
     scale = 1.0 / math.sqrt(d)
@@ -289,9 +300,15 @@ def bench_config5(torch, _hip, steps=64, seed=500):
         _hip.kv_append(kc, vc, nk, nv, start_dev=starts)
 
     def decode(i):
-        _, _, _, seqlens, maxlen, q, out, splits, ws = plan[i]
+        _, _, _, seqlens, maxlen, q, out, splits, ws, _ = plan[i]
         _hip.decode(q, kc[:, :, :maxlen], vc[:, :, :maxlen], out, None, seqlens, scale=scale,
                     num_splits=splits, workspace=ws)
+
+    def fused_step(i):
+        nk, nv, q = plan[i][0], plan[i][1], plan[i][5]
+        prev, maxprev, fsplits, fws, fout = plan[i][9]
+        _hip.append_decode(q, kc, vc, nk, nv, fout, None, prev, past_length=0,
+                           max_length=maxprev, scale=scale, num_splits=fsplits, workspace=fws)
 
     def timed(fn):
         # Captured into a HIP graph so the figure is GPU time, not the
@@ -317,8 +334,14 @@ def bench_config5(torch, _hip, steps=64, seed=500):
     both = timed(lambda: [f(i) for i in range(steps) for f in (append, decode)])
     app = timed(lambda: [append(i) for i in range(steps)])
     dec = timed(lambda: [decode(i) for i in range(steps)])
+    fused = timed(lambda: [fused_step(i) for i in range(steps)])
     if not all(bool(torch.isfinite(p[6]).all()) for p in plan):
         raise RuntimeError("config 5: non-finite decode output")
+    # The fused outputs must agree with the two-launch path's (fp16 O,
+    # atol = rtol = 2e-3; the split partitions differ).
+    for p in plan:
+        if not torch.allclose(p[9][4].float(), p[6].float(), atol=2e-3, rtol=2e-3):
+            raise RuntimeError("config 5: fused append + decode differs from append, decode")
     return {"workload": "BASELINE config 5: cache [8,8,32768,64] fp16, lengths U[4096,28000], "
                         f"{steps} steps of append n in [1,16] + ragged decode Hq=32",
             "steps": steps, "tokens_appended": sum(ns), "us_total": both,
@@ -330,6 +353,12 @@ def bench_config5(torch, _hip, steps=64, seed=500):
                        "hbm_gbps": dec_bytes / (dec * 1e-6) / 1e9,
                        "hbm_frac": dec_bytes / (dec * 1e-6) / PEAK_HBM,
                        "us_per_token": dec / sum(ns)},
+            "fused_append_decode": {
+                "us_per_step": fused / steps, "bytes": app_bytes // 2 + dec_bytes,
+                "hbm_gbps": (app_bytes // 2 + dec_bytes) / (fused * 1e-6) / 1e9,
+                "hbm_frac": (app_bytes // 2 + dec_bytes) / (fused * 1e-6) / PEAK_HBM,
+                "note": "kf_attn_append_decode: new tokens read once from their buffer, "
+                        "written once to the cache; no append launch"},
             "timing": "64 staged steps captured in one HIP graph, one replay between two HIP "
                       "events (after a warm replay)"}
 

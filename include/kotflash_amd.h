@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define KF_ABI_VERSION 2
+#define KF_ABI_VERSION 3
 
 enum kf_status {
   KF_OK = 0,
@@ -170,6 +170,36 @@ int kf_kv_append(void* k_cache, void* v_cache, const void* new_k, const void* ne
                  int64_t D, int64_t capacity, const int64_t* k_cache_strides,
                  const int64_t* v_cache_strides, const int64_t* new_k_strides4,
                  const int64_t* new_v_strides4, int dtype, void* stream);
+
+/*
+ * Fused append + split-KV decode in one decode launch (plus the merge):
+ * new tokens new_k/new_v [B, Hkv, Snew, D] are stored at cache positions
+ * start_b .. start_b + Snew - 1, and query rows of batch entry b attend,
+ * non-causally, to cache keys [0, start_b) followed by the Snew new keys,
+ * i.e. to the first start_b + Snew positions of the cache after the append.
+ * start_b = lengths[b] (device int32 [B], nullable: then start_b =
+ * past_length for every b, and past_length must equal max_length).
+ * max_length >= max_b start_b (host-side) sizes the splits over the old keys
+ * (num_splits from kf_decode_num_splits / _ragged over those lengths; 0 keys
+ * allowed); one more split reads the new tokens from their own buffer and a
+ * single workgroup per (b, kv_head) writes them into the cache (bit-exact).
+ * Workspace: kf_decode_workspace_bytes(..., num_splits + 1). Positions at or
+ * beyond `capacity` are not written (callers validate first, as the
+ * reference does). Caches, q, new_k/new_v and o need a unit head_dim stride.
+ * Replaces attention_forward_strided_append + _strided_decode_append_split
+ * (reference kotflash/kernels/triton_decode.py:302-386, :108-238), which
+ * folds one token's slot write into its split kernel; here Snew >= 1 tokens
+ * and per-sequence positions.
+ */
+int kf_attn_append_decode(const void* q, void* k_cache, void* v_cache, const void* new_k,
+                          const void* new_v, void* o, float* lse, const int32_t* lengths,
+                          int64_t past_length, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq,
+                          int64_t Snew, int64_t max_length, int64_t capacity, int64_t D,
+                          const int64_t* q_strides, const int64_t* k_cache_strides,
+                          const int64_t* v_cache_strides, const int64_t* new_k_strides,
+                          const int64_t* new_v_strides, const int64_t* o_strides, float scale,
+                          int num_splits, int dtype, void* workspace, size_t workspace_bytes,
+                          void* stream);
 
 #ifdef __cplusplus
 }

@@ -19,7 +19,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libkotflash_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 KF_F16, KF_BF16 = 0, 1
 KF_BWD_DELTA, KF_BWD_DQ, KF_BWD_DKDV, KF_BWD_DKDV_FIXUP = 1, 2, 4, 8
 KF_BWD_ALL = KF_BWD_DELTA | KF_BWD_DQ | KF_BWD_DKDV | KF_BWD_DKDV_FIXUP
@@ -51,6 +51,9 @@ _SIGNATURES = {
                             _I64P, _I64P, _I64P, _I64P, _F, _I, _I, _P, _SZ, _P]),
     "kf_kv_append": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                           _I64P, _I64P, _I64P, _I64P, _I, _P]),
+    "kf_attn_append_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
+                                   _I64, _I64, _I64, _I64, _I64P, _I64P, _I64P, _I64P, _I64P,
+                                   _I64P, _F, _I, _I, _P, _SZ, _P]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -257,3 +260,23 @@ def kv_append(k_cache, v_cache, new_k, new_v, *, start: int = 0,
             dtype_code(k_cache.dtype), _stream(k_cache.device),
         )
     _check(rc, "kf_kv_append")
+
+
+def append_decode(q, k_cache, v_cache, new_k, new_v, out, lse: Optional[torch.Tensor],
+                  lengths: Optional[torch.Tensor], *, past_length: int, max_length: int,
+                  scale: float, num_splits: int, workspace: torch.Tensor) -> None:
+    """kf_attn_append_decode: store new_k/new_v at each sequence's position
+    and decode over the old keys plus the new ones, in one decode launch."""
+    b, hq, sq, d = q.shape
+    _, hkv, capacity, _ = k_cache.shape
+    keep = [_strides(t) for t in (q, k_cache, v_cache, new_k, new_v, out)]
+    with _DeviceGuard(q.device):
+        rc = lib().kf_attn_append_decode(
+            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), new_k.data_ptr(),
+            new_v.data_ptr(), out.data_ptr(), lse.data_ptr() if lse is not None else None,
+            lengths.data_ptr() if lengths is not None else None, int(past_length),
+            b, hq, hkv, sq, new_k.shape[2], int(max_length), capacity, d, *keep,
+            float(scale), int(num_splits), dtype_code(q.dtype), workspace.data_ptr(),
+            workspace.numel() * workspace.element_size(), _stream(q.device),
+        )
+    _check(rc, "kf_attn_append_decode")

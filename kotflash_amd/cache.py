@@ -277,6 +277,65 @@ class RaggedKVCache(PreallocatedKVCache):
                 self.v[b, :, start:start + n].copy_(new_v[b])
         self._set([x + n for x in self.lengths])
 
+    def append_and_attend(self, q_new, new_k, new_v, *, append_backend: str = "auto",
+                          attention_backend: str = "auto") -> torch.Tensor:
+        """Append n tokens to every sequence, then attend, non-causally, with
+        q_new [B, Hq, Sq, D] over each sequence's first lengths[b] + n
+        positions.
+
+        ``append_backend="fused"`` stores the new tokens from inside the
+        split-KV decode (one decode launch and the merge, no append launch;
+        inference only). ``"auto"`` takes it when the HIP decode applies
+        (gfx950, fp16/bf16, head_dim a multiple of 8, no autograd) and
+        ``attention_backend`` is "auto" or "hip"; otherwise it appends
+        (``append``) and attends (``attend``) as two steps.
+        """
+        if attention_backend not in ("auto", "hip", "triton", "sdpa"):
+            raise ValueError("attention backend must be one of: auto, hip, triton or sdpa")
+        if append_backend not in ("auto", "torch", "hip", "cuda", "fused"):
+            raise ValueError("append backend must be one of: auto, torch, hip, cuda or fused")
+        self._check_new(new_k, new_v)
+        if not isinstance(q_new, torch.Tensor) or q_new.ndim != 4:
+            raise ValueError("q must use [B, Hq, Sq, D] layout")
+        if q_new.shape[0] != self.k.shape[0] or q_new.shape[-1] != self.k.shape[-1]:
+            raise ValueError("Query batch and head dimension must match the cache")
+        if q_new.shape[1] <= 0 or q_new.shape[1] % self.k.shape[1] != 0:
+            raise ValueError("Query heads must be non-zero and divisible by the cache KV-head count")
+        if q_new.device != self.k.device or q_new.dtype != self.k.dtype:
+            raise ValueError("Query device and dtype must match the cache")
+        n = new_k.shape[2]
+        full = [b for b, x in enumerate(self.lengths) if x + n > self.max_len]
+        if full:
+            b = full[0]
+            raise ValueError(
+                f"KV cache full: sequence {b} has {self.lengths[b]} + {n} tokens "
+                f"exceeding max_len={self.max_len}"
+            )
+        has_grad = torch.is_grad_enabled() and any(
+            t.requires_grad for t in (q_new, new_k, new_v)
+        )
+        fusable = (q_new.is_cuda and q_new.dtype in (torch.float16, torch.bfloat16)
+                   and q_new.shape[-1] % 8 == 0 and _hip.is_gfx950(q_new.device)
+                   and _hip.library_available())
+        fused = append_backend == "fused" or (
+            append_backend == "auto" and fusable and not has_grad
+            and attention_backend in ("auto", "hip", "triton"))
+        if fused:
+            if attention_backend == "sdpa":
+                raise ValueError("append_backend='fused' requires attention_backend='auto' or 'hip'")
+            if has_grad:
+                raise RuntimeError("append_backend='fused' is inference-only; disable gradients")
+            from .kernels.hip_decode import attention_append_decode_ragged
+
+            out = attention_append_decode_ragged(
+                q_new, self.k, self.v, new_k, new_v, self.seqlens, host_lengths=self.lengths,
+                scale=1.0 / (q_new.shape[-1] ** 0.5),
+            )
+            self._set([x + n for x in self.lengths])
+            return out
+        self.append(new_k, new_v, backend=append_backend)
+        return self.attend(q_new, backend=attention_backend)
+
     def view(self, b: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
         """Storage-backed [1, Hkv, lengths[b], D] views of sequence b."""
         if self.lengths[b] == 0:

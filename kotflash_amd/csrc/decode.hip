@@ -52,6 +52,13 @@ struct DecParams {
   float* part_o;    // [ngroups][nsplit][RB][D]
   float* part_lse;  // [ngroups][nsplit][RB]
   const int32_t* seqlens;
+  // Fused append (decode_kernel<..., true>): the new tokens [B][Hkv][nnew][D]
+  // and the cache capacity; k/v above are then the caches themselves.
+  const uint16_t* nk;
+  const uint16_t* nv;
+  int64_t nk_sb, nk_sh, nk_ss;
+  int64_t nv_sb, nv_sh, nv_ss;
+  int nnew, capacity;
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;
@@ -65,7 +72,7 @@ struct DecParams {
 // turn, so chunks are whole multiples of 128 keys.
 constexpr int kDecGranule = 128;
 
-template <typename T, int DT, int QB>
+template <typename T, int DT, int QB, bool APPEND>
 __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   constexpr int CPR = DT / 8;          // 16-byte chunks per row
   constexpr int NDC = DT / 32;         // 32-wide head-dim chunks (S contraction)
@@ -100,8 +107,17 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   const int R = p.G * p.Sq;
 
   const int L = p.seqlens ? min(max(p.seqlens[b], 0), p.Sk) : p.Sk;
-  const int c0 = split * p.chunk;
-  const int c1 = min(c0 + p.chunk, L);
+  // With APPEND, the last split attends to the nnew new tokens, read from
+  // their own buffer (keys [0, nnew) of it); the others cover the cache's
+  // keys [0, L_b) as without it. No workgroup of the launch reads cache rows
+  // [L_b, L_b + nnew), so the new split's copy into them races with nothing.
+  const bool fresh = APPEND && split == p.nsplit - 1;
+  const int c0 = fresh ? 0 : split * p.chunk;
+  const int c1 = fresh ? p.nnew : min(c0 + p.chunk, L);
+  const uint16_t* kbase = fresh ? p.nk + b * p.nk_sb + kvh * p.nk_sh : p.k + b * p.k_sb + kvh * p.k_sh;
+  const uint16_t* vbase = fresh ? p.nv + b * p.nv_sb + kvh * p.nv_sh : p.v + b * p.v_sb + kvh * p.v_sh;
+  const int64_t kss = fresh ? p.nk_ss : p.k_ss;
+  const int64_t vss = fresh ? p.nv_ss : p.v_ss;
   // This wave's steps: 32-key blocks c0 + 32 (wave + 4 j), j = 0 .. nst - 1.
   const int nst = c1 > c0 + 32 * wave ? cdiv(c1 - c0 - 32 * wave, 128) : 0;
   const int nrow = min(RB, R - rb * RB);
@@ -120,8 +136,8 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
 
   // K/V resources end at the chunk's last visible key: keys at or beyond c1
   // (the range check includes the scalar offset) load as zeros.
-  const auto kr = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, rows_extent(c1, p.k_ss, p.D));
-  const auto vr = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, rows_extent(c1, p.v_ss, p.D));
+  const auto kr = make_rsrc(kbase, rows_extent(c1, kss, p.D));
+  const auto vr = make_rsrc(vbase, rows_extent(c1, vss, p.D));
   const auto qr = make_rsrc(p.q + b * p.q_sb + kvh * p.G * p.q_sh,
                             (uint32_t)((((int64_t)p.G - 1) * p.q_sh + ((int64_t)p.Sq - 1) * p.q_ss + p.D) * 2));
   uint16_t* qs = reinterpret_cast<uint16_t*>(smem);                 // [RB][DT], swizzled
@@ -152,8 +168,8 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
     const int r = pc / CPR;
     const int c = (pc % CPR) ^ Tile::key(r);
     const bool ok = c * 8 < p.D;
-    koff[k] = ok ? (uint32_t)(r * p.k_ss + c * 8) * 2u : kOOB;
-    voff[k] = ok ? (uint32_t)(r * p.v_ss + c * 8) * 2u : kOOB;
+    koff[k] = ok ? (uint32_t)(r * kss + c * 8) * 2u : kOOB;
+    voff[k] = ok ? (uint32_t)(r * vss + c * 8) * 2u : kOOB;
   }
   const uint32_t ring0 = lds_addr(kvring);
   // Step j of this wave: its K and V tiles (32 keys) into the wave's LDS
@@ -162,8 +178,8 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   auto issue = [&](int j, auto slot_c) {
     constexpr int slot = decltype(slot_c)::value;
     const int kb0 = c0 + 32 * (wave + 4 * j);
-    const uint32_t kso = (uint32_t)kb0 * (uint32_t)(p.k_ss * 2);
-    const uint32_t vso = (uint32_t)kb0 * (uint32_t)(p.v_ss * 2);
+    const uint32_t kso = (uint32_t)kb0 * (uint32_t)(kss * 2);
+    const uint32_t vso = (uint32_t)kb0 * (uint32_t)(vss * 2);
     const uint32_t m0 = ring0 + (uint32_t)(slot * 2 * VT * 2);
 #pragma unroll
     for (int k = 0; k < NVI; ++k) {
@@ -365,6 +381,26 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
       if (d == 0) p.part_lse[pbase + r] = lse_val;
     }
   }
+  if constexpr (APPEND) {
+    // The single owner of the append: the new split of row block 0 stores
+    // new[b, kvh, t, :] to cache position seqlens[b] + t (t < nnew) in
+    // 16-byte vectors, after its own loads of the new tokens (bit-exact copy).
+    // Positions at or beyond the capacity are not written (callers check).
+    if (fresh && rb == 0) {
+      const int start = p.seqlens ? max(p.seqlens[b], 0) : p.Sk;
+      const int cpr = p.D / 8;
+      uint16_t* kc = const_cast<uint16_t*>(p.k) + b * p.k_sb + kvh * p.k_sh;
+      uint16_t* vc = const_cast<uint16_t*>(p.v) + b * p.v_sb + kvh * p.v_sh;
+      for (int e = tid; e < p.nnew * cpr; e += 256) {
+        const int t = e / cpr, d = (e % cpr) * 8;
+        if (start + t >= p.capacity) continue;
+        const uint4 kv4 = *reinterpret_cast<const uint4*>(kbase + t * kss + d);
+        const uint4 vv4 = *reinterpret_cast<const uint4*>(vbase + t * vss + d);
+        *reinterpret_cast<uint4*>(kc + (int64_t)(start + t) * p.k_ss + d) = kv4;
+        *reinterpret_cast<uint4*>(vc + (int64_t)(start + t) * p.v_ss + d) = vv4;
+      }
+    }
+  }
 }
 
 // Merge of the split partials: one wave per output row, no LDS and no
@@ -466,7 +502,7 @@ static int decode_rows_per_wg(int64_t G, int64_t Sq) {
   return R <= 16 ? 16 : R <= 32 ? 32 : 64;
 }
 
-template <typename T, int DT>
+template <typename T, int DT, bool APPEND>
 static int launch_decode(DecParams p, hipStream_t stream) {
   const int R = p.G * p.Sq;
   p.rb_rows = decode_rows_per_wg(p.G, p.Sq);
@@ -474,9 +510,9 @@ static int launch_decode(DecParams p, hipStream_t stream) {
   const int64_t grid = (int64_t)p.nsplit * p.nrb * p.B * p.Hkv;
   if (grid > 0x7fffffff) return set_error(KF_EUNSUPPORTED, "kf_attn_decode: grid too large");
   switch (p.rb_rows) {
-    case 16: hipLaunchKernelGGL((decode_kernel<T, DT, 1>), dim3((unsigned)grid), dim3(256), 0, stream, p); break;
-    case 32: hipLaunchKernelGGL((decode_kernel<T, DT, 2>), dim3((unsigned)grid), dim3(256), 0, stream, p); break;
-    default: hipLaunchKernelGGL((decode_kernel<T, DT, 4>), dim3((unsigned)grid), dim3(256), 0, stream, p); break;
+    case 16: hipLaunchKernelGGL((decode_kernel<T, DT, 1, APPEND>), dim3((unsigned)grid), dim3(256), 0, stream, p); break;
+    case 32: hipLaunchKernelGGL((decode_kernel<T, DT, 2, APPEND>), dim3((unsigned)grid), dim3(256), 0, stream, p); break;
+    default: hipLaunchKernelGGL((decode_kernel<T, DT, 4, APPEND>), dim3((unsigned)grid), dim3(256), 0, stream, p); break;
   }
   int rc = check_launch("kf_attn_decode(split)");
   if (rc || p.nsplit == 1) return rc;
@@ -488,13 +524,13 @@ static int launch_decode(DecParams p, hipStream_t stream) {
   return check_launch("kf_attn_decode(merge)");
 }
 
-template <typename T>
+template <typename T, bool APPEND>
 static int dispatch_decode(const DecParams& p, hipStream_t stream) {
   switch (head_tile(p.D)) {
-    case 32: return launch_decode<T, 32>(p, stream);
-    case 64: return launch_decode<T, 64>(p, stream);
-    case 96: return launch_decode<T, 96>(p, stream);
-    default: return launch_decode<T, 128>(p, stream);
+    case 32: return launch_decode<T, 32, APPEND>(p, stream);
+    case 64: return launch_decode<T, 64, APPEND>(p, stream);
+    case 96: return launch_decode<T, 96, APPEND>(p, stream);
+    default: return launch_decode<T, 128, APPEND>(p, stream);
   }
 }
 
@@ -612,5 +648,82 @@ extern "C" int kf_attn_decode(const void* q, const void* k, const void* v, void*
   p.chunk = (int)chunk;
   p.scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  return dtype == KF_F16 ? dispatch_decode<_Float16>(p, s) : dispatch_decode<__bf16>(p, s);
+  return dtype == KF_F16 ? dispatch_decode<_Float16, false>(p, s) : dispatch_decode<__bf16, false>(p, s);
+}
+
+extern "C" int kf_attn_append_decode(const void* q, void* k_cache, void* v_cache, const void* new_k,
+                                     const void* new_v, void* o, float* lse,
+                                     const int32_t* lengths, int64_t past_length, int64_t B,
+                                     int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Snew,
+                                     int64_t max_length, int64_t capacity, int64_t D,
+                                     const int64_t* q_strides, const int64_t* k_cache_strides,
+                                     const int64_t* v_cache_strides, const int64_t* new_k_strides,
+                                     const int64_t* new_v_strides, const int64_t* o_strides,
+                                     float scale, int num_splits, int dtype, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  const char* what = "kf_attn_append_decode";
+  // Sizes are checked as for kf_attn_decode with the cache's own keys
+  // (max_length, at least 1 for the check) and the new tokens both present.
+  int rc = check_attn_common(what, B, Hq, Hkv, Sq, max_length > 0 ? max_length : 1, D, dtype);
+  if (rc) return rc;
+  if ((rc = check_tensor(what, "q", q, q_strides)) ||
+      (rc = check_tensor(what, "k_cache", k_cache, k_cache_strides)) ||
+      (rc = check_tensor(what, "v_cache", v_cache, v_cache_strides)) ||
+      (rc = check_tensor(what, "new_k", new_k, new_k_strides)) ||
+      (rc = check_tensor(what, "new_v", new_v, new_v_strides)) ||
+      (rc = check_tensor(what, "o", o, o_strides)))
+    return rc;
+  if (!(scale == scale) || scale - scale != 0.f) return set_error(KF_EINVAL, "%s: scale must be finite", what);
+  if (Snew <= 0 || Snew > 0x3fffffff) return set_error(KF_EINVAL, "%s: Snew must be positive", what);
+  if (max_length < 0 || capacity <= 0 || capacity > 0x3fffffff || max_length > capacity)
+    return set_error(KF_EINVAL, "%s: need 0 <= max_length <= capacity", what);
+  if (lengths == nullptr && (past_length != max_length || past_length + Snew > capacity))
+    return set_error(KF_EINVAL, "%s: past_length %lld + %lld new tokens must fit capacity %lld "
+                     "(and equal max_length without per-sequence lengths)", what,
+                     (long long)past_length, (long long)Snew, (long long)capacity);
+  if (num_splits < 1) return set_error(KF_EINVAL, "%s: num_splits must be >= 1", what);
+  const int64_t stage = kDecGranule;
+  const int64_t Sk = max_length > 0 ? max_length : 1;
+  const int64_t chunk = ((Sk + num_splits - 1) / num_splits + stage - 1) / stage * stage;
+  if ((Sk + chunk - 1) / chunk != num_splits)
+    return set_error(KF_EINVAL, "%s: num_splits=%d does not partition max_length=%lld into whole "
+                     "%lld-key stages (use kf_decode_num_splits)", what, num_splits,
+                     (long long)max_length, (long long)stage);
+  if (((Hq / Hkv - 1) * q_strides[1] + (Sq - 1) * q_strides[2] + D) * 2 > 0x7fffffffLL)
+    return set_error(KF_EUNSUPPORTED, "%s: one KV group of q spans more than 2 GiB", what);
+  // One more split (the new tokens) than the cache's own.
+  const size_t need = kf_decode_workspace_bytes(B, Hq, Hkv, Sq, D, num_splits + 1);
+  if (workspace == nullptr || workspace_bytes < need)
+    return set_error(KF_EINVAL, "%s: workspace of %zu bytes required, got %zu", what, need,
+                     workspace == nullptr ? (size_t)0 : workspace_bytes);
+  if ((rc = check_extent(what, "k_cache", capacity, k_cache_strides[2], D)) ||
+      (rc = check_extent(what, "v_cache", capacity, v_cache_strides[2], D)) ||
+      (rc = check_extent(what, "new_k", Snew, new_k_strides[2], D)) ||
+      (rc = check_extent(what, "new_v", Snew, new_v_strides[2], D)))
+    return rc;
+  DecParams p{};
+  p.q = (const uint16_t*)q; p.k = (const uint16_t*)k_cache; p.v = (const uint16_t*)v_cache;
+  p.nk = (const uint16_t*)new_k; p.nv = (const uint16_t*)new_v;
+  p.o = (uint16_t*)o; p.lse = lse; p.seqlens = lengths;
+  const int64_t G = Hq / Hkv;
+  const size_t slots = (size_t)(B * Hkv * decode_row_blocks(G, Sq)) * (num_splits + 1) *
+                       decode_rows_per_wg(G, Sq);
+  p.part_o = (float*)workspace;
+  p.part_lse = (float*)((char*)workspace + (slots * (size_t)D * sizeof(float) + 255) / 256 * 256);
+  p.q_sb = q_strides[0]; p.q_sh = q_strides[1]; p.q_ss = q_strides[2];
+  p.k_sb = k_cache_strides[0]; p.k_sh = k_cache_strides[1]; p.k_ss = k_cache_strides[2];
+  p.v_sb = v_cache_strides[0]; p.v_sh = v_cache_strides[1]; p.v_ss = v_cache_strides[2];
+  p.nk_sb = new_k_strides[0]; p.nk_sh = new_k_strides[1]; p.nk_ss = new_k_strides[2];
+  p.nv_sb = new_v_strides[0]; p.nv_sh = new_v_strides[1]; p.nv_ss = new_v_strides[2];
+  p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
+  p.B = (int)B; p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.Sq = (int)Sq; p.D = (int)D;
+  p.Sk = (int)max_length;  // per-sequence lengths are clamped to it; 0 = no cache keys
+  p.G = (int)G;
+  p.nsplit = num_splits + 1;
+  p.chunk = (int)chunk;
+  p.nnew = (int)Snew;
+  p.capacity = (int)capacity;
+  p.scale_log2 = scale * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  return dtype == KF_F16 ? dispatch_decode<_Float16, true>(p, s) : dispatch_decode<__bf16, true>(p, s);
 }

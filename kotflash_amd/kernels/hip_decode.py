@@ -77,10 +77,12 @@ def attention_forward_strided_append(q, k_cache, v_cache, new_k, new_v, *,
     """Append one token at ``past_length`` and attend over the first
     ``past_length + 1`` cache positions; returns O.
 
-    Same contract as the reference (triton_decode.py:302-386). The reference
-    folds the slot write into its split kernel; here the append is its own
-    16-byte-vector copy launch followed by the split-KV decode, which reads
-    the freshly written slot from the cache.
+    Same contract as the reference (triton_decode.py:302-386): two launches,
+    a split kernel that also writes the slot and the LSE merge. The split
+    kernel's last split attends to the new token straight from ``new_k`` /
+    ``new_v`` and stores it into the cache (``kf_attn_append_decode``); the
+    other splits read positions [0, past_length) in place. Head dims that are
+    not a multiple of 8 take a separate append launch and a padded decode.
     """
     require_hip_tensors("fused append/decode", q, k_cache, v_cache, new_k, new_v)
     if q.ndim != 4 or q.shape[2] != 1:
@@ -97,6 +99,10 @@ def attention_forward_strided_append(q, k_cache, v_cache, new_k, new_v, *,
         raise ValueError("query, cache and new K/V shapes are incompatible")
     if hq % hkv or past_length < 0 or past_length + 1 > capacity:
         raise ValueError("unsupported head grouping, cache length or capacity")
+    if d % 8 == 0 and all(_hip.layout_ok(t) for t in (q, k_cache, v_cache)):
+        new_k, new_v = (t if _hip.layout_ok(t) else t.contiguous() for t in (new_k, new_v))
+        return _append_decode(q, k_cache, v_cache, new_k, new_v, None, past_length,
+                              past_length, float(scale), with_lse=False)[0]
     _hip.kv_append(k_cache, v_cache, new_k, new_v, start=past_length)
     k_view = k_cache[:, :, : past_length + 1]
     v_view = v_cache[:, :, : past_length + 1]
@@ -105,6 +111,61 @@ def attention_forward_strided_append(q, k_cache, v_cache, new_k, new_v, *,
         q, k_view, v_view = (prepare(t, dp) for t in (q, k_view, v_view))
     out = _decode(q, k_view, v_view, None, float(scale), with_lse=False)[0]
     return out[..., :d].contiguous() if dp != d else out
+
+
+def _append_decode(q, k_cache, v_cache, new_k, new_v, lengths: Optional[torch.Tensor],
+                   past_length: int, max_length: int, scale: float, with_lse: bool,
+                   host_lengths: Optional[Sequence[int]] = None):
+    b, hq, sq, d = q.shape
+    hkv = k_cache.shape[1]
+    out = torch.empty((b, hq, sq, d), device=q.device, dtype=q.dtype)
+    lse = torch.empty((b, hq, sq), device=q.device, dtype=torch.float32) if with_lse else None
+    if host_lengths is not None and max_length > 0:
+        splits = _hip.decode_num_splits_ragged(b, hq, hkv, sq, host_lengths, d)
+    else:
+        splits = _hip.decode_num_splits(b, hq, hkv, sq, max_length, d)
+    nbytes = _hip.decode_workspace_bytes(b, hq, hkv, sq, d, splits + 1)
+    ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
+    _hip.append_decode(q, k_cache, v_cache, new_k, new_v, out, lse, lengths,
+                       past_length=past_length, max_length=max_length, scale=scale,
+                       num_splits=splits, workspace=ws)
+    return out, lse
+
+
+def attention_append_decode_ragged(q, k_cache, v_cache, new_k, new_v, seqlens: torch.Tensor, *,
+                                   host_lengths: Sequence[int], scale: float,
+                                   with_lse: bool = False):
+    """Append new_k/new_v [B, Hkv, n, D] at each sequence's position
+    ``seqlens[b]`` (device int32 [B], equal to ``host_lengths``) and run
+    non-causal decode in which the rows of sequence b see its first
+    seqlens[b] + n positions after the append: one decode launch and one
+    merge (``kf_attn_append_decode``). Callers validate capacity first.
+    Returns O, or (O, LSE) with ``with_lse``."""
+    require_hip_tensors("ragged append/decode", q, k_cache, v_cache, new_k, new_v)
+    if seqlens.dtype != torch.int32 or seqlens.device != q.device or seqlens.shape != (q.shape[0],):
+        raise ValueError("seqlens must be a device int32 tensor of shape [B]")
+    if q.ndim != 4 or k_cache.ndim != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError("expected [B,H,S,D] query and cache tensors")
+    if new_k.ndim != 4 or new_v.shape != new_k.shape or new_k.shape[2] <= 0:
+        raise ValueError("new K/V must have matching non-empty [B,Hkv,n,D] shapes")
+    b, hq, _, d = q.shape
+    _, hkv, capacity, _ = k_cache.shape
+    if k_cache.shape[0] != b or hq % hkv or k_cache.shape[3] != d or new_k.shape[:2] != (b, hkv) \
+            or new_k.shape[3] != d:
+        raise ValueError("query, cache and new K/V shapes are incompatible")
+    if d % 8 or not gfx950_head_dim_ok(d):
+        raise ValueError("ragged append/decode needs head_dim a multiple of 8 in [8, 128]")
+    host_lengths = [int(x) for x in host_lengths]
+    if len(host_lengths) != b:
+        raise ValueError("host_lengths must have one entry per batch element")
+    if min(host_lengths) < 0 or max(host_lengths) + new_k.shape[2] > capacity:
+        raise ValueError("appended tokens must fit the cache capacity")
+    if not all(_hip.layout_ok(t) for t in (q, k_cache, v_cache)):
+        raise ValueError("ragged append/decode needs inner-contiguous, 16-byte aligned tensors")
+    new_k, new_v = (t if _hip.layout_ok(t) else t.contiguous() for t in (new_k, new_v))
+    out, lse = _append_decode(q, k_cache, v_cache, new_k, new_v, seqlens, 0, max(host_lengths),
+                              float(scale), with_lse=with_lse, host_lengths=host_lengths)
+    return (out, lse) if with_lse else out
 
 
 def attention_decode_ragged(q, k_cache, v_cache, seqlens: torch.Tensor, *, max_seqlen: int,

@@ -134,3 +134,44 @@ def test_ragged_decode_planner():
     assert 700 <= nonempty <= 1400
     assert plan([0, 0]) == 1
     assert lib.kf_decode_num_splits_ragged(2, 8, 2, 1, None, 64) == 1
+
+
+def _append_decode(lib, **kw):
+    a = dict(q=0x1000, kc=0x2000, vc=0x3000, nk=0x4000, nv=0x5000, o=0x6000, lengths=None, past=100,
+             B=1, Hq=4, Hkv=1, Sq=1, Snew=1, max_length=100, capacity=128, D=64, scale=0.125,
+             splits=1, ws=0x7000, ws_bytes=1 << 20)
+    a.update(kw)
+    s = _arr(128 * 64, 128 * 64, 64)
+    return lib.kf_attn_append_decode(a["q"], a["kc"], a["vc"], a["nk"], a["nv"], a["o"], None,
+                                     a["lengths"], a["past"], a["B"], a["Hq"], a["Hkv"], a["Sq"],
+                                     a["Snew"], a["max_length"], a["capacity"], a["D"],
+                                     s, s, s, s, s, s, a["scale"], a["splits"], 0, a["ws"],
+                                     a["ws_bytes"], None)
+
+
+@pytest.mark.parametrize("kwargs,match", [
+    (dict(past=128, max_length=128), "capacity"),          # no room for the new token
+    (dict(past=99), "past_length"),                        # scalar position != max_length
+    (dict(max_length=129), "max_length <= capacity"),
+    (dict(Snew=0), "Snew"),
+    (dict(nk=None), "new_k is null"),
+    (dict(kc=0x2008), "aligned"),
+    (dict(ws=None), "workspace"),
+    (dict(ws_bytes=16), "workspace"),
+    (dict(splits=2, max_length=100, past=100), "partition"),
+    (dict(D=76), "multiple of 8"),
+])
+def test_append_decode_argument_validation(kwargs, match):
+    lib = _hip.lib()
+    rc = _append_decode(lib, **kwargs)
+    assert rc == 1 or rc == 2
+    assert match in lib.kf_last_error().decode()
+
+
+def test_append_decode_workspace_has_one_extra_split():
+    lib = _hip.lib()
+    ns = lib.kf_decode_num_splits(8, 32, 8, 16, 28000, 64)
+    assert (lib.kf_decode_workspace_bytes(8, 32, 8, 16, 64, ns + 1)
+            > lib.kf_decode_workspace_bytes(8, 32, 8, 16, 64, ns))
+    # Zero cache keys: one (empty) cache split plus the new tokens' split.
+    assert lib.kf_decode_num_splits(1, 4, 1, 1, 0, 64) == 1

@@ -167,3 +167,33 @@ def test_ragged_cache_attend_matches_per_sequence_sdpa():
         torch.testing.assert_close(out[b:b + 1], exp)
     with pytest.raises(ValueError, match="lengths"):
         cache.set_lengths([1, 13])
+
+
+def test_ragged_cache_append_and_attend_two_step_path_on_cpu():
+    """On the CPU, append_and_attend appends with torch copies and attends per
+    sequence with SDPA; the fused path is GPU-only and refuses SDPA, and a
+    rejected append leaves lengths and storage untouched."""
+    torch.manual_seed(6)
+    cache = RaggedKVCache(2, 1, 9, 8, device="cpu", dtype=torch.float32)
+    cache.k.normal_()
+    cache.v.normal_()
+    cache.set_lengths([2, 5])
+    nk, nv = torch.randn(2, 1, 3, 8), torch.randn(2, 1, 3, 8)
+    q = torch.randn(2, 2, 3, 8)
+    out = cache.append_and_attend(q, nk, nv)
+    assert cache.lengths == [5, 8]
+    for b, n in enumerate([5, 8]):
+        torch.testing.assert_close(cache.k[b, :, n - 3:n], nk[b])
+        exp = F.scaled_dot_product_attention(
+            q[b:b + 1], cache.k[b:b + 1, :, :n].repeat_interleave(2, 1),
+            cache.v[b:b + 1, :, :n].repeat_interleave(2, 1))
+        torch.testing.assert_close(out[b:b + 1], exp)
+    before = cache.k.clone()
+    with pytest.raises(ValueError, match="full"):
+        cache.append_and_attend(q, nk, nv)
+    assert cache.lengths == [5, 8] and torch.equal(cache.k, before)
+    with pytest.raises(ValueError, match="fused"):
+        cache.append_and_attend(q[:, :, :1], nk[:, :, :1], nv[:, :, :1], append_backend="fused",
+                                attention_backend="sdpa")
+    with pytest.raises(ValueError, match="append backend"):
+        cache.append_and_attend(q, nk, nv, append_backend="nope")

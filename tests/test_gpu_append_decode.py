@@ -1,0 +1,150 @@
+"""Fused append + split-KV decode (kf_attn_append_decode) on the GPU.
+
+One decode launch stores the new tokens into the cache and attends over the
+old keys plus the new ones (reference kotflash/kernels/triton_decode.py:
+302-386 folds one token's slot write into its split kernel the same way).
+Checked here:
+- the cache after the call equals slice assignment, bit for bit, with every
+  other slot (NaN sentinels) untouched;
+- O and LSE against dense fp32 attention over each sequence's first
+  L_b + n positions (fp16 atol = rtol = 2e-3, bf16 1e-2);
+- ragged lengths including 0, granule boundaries (127, 128, 129) and a
+  sequence that fills the cache to capacity; n in 1..16, Sq = 1 and Sq = n;
+- the scalar entry (attention_forward_strided_append) and the cache classes.
+"""
+import pytest
+import torch
+
+from kotflash_amd.cache import RaggedKVCache
+from kotflash_amd.kernels.hip_decode import (attention_append_decode_ragged,
+                                             attention_decode_ragged,
+                                             attention_forward_strided_append)
+from tests.gpu_helpers import FWD_TOL, assert_close, reference_fp32, seeded
+
+pytestmark = pytest.mark.gpu
+F16, BF16 = torch.float16, torch.bfloat16
+
+
+def _nan_cache(b, hkv, cap, d, dtype, lengths, seed):
+    kc = torch.full((b, hkv, cap, d), float("nan"), device="cuda", dtype=dtype)
+    vc = torch.full_like(kc, float("nan"))
+    for i, n in enumerate(lengths):
+        if n:
+            kc[i, :, :n] = seeded((hkv, n, d), seed + 2 * i, dtype=dtype)
+            vc[i, :, :n] = seeded((hkv, n, d), seed + 2 * i + 1, dtype=dtype)
+    return kc, vc
+
+
+def _bits(t):
+    return t.view(torch.int16)
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("n,sq", [(1, 1), (5, 5), (16, 16), (16, 1)])
+def test_ragged_append_decode(dtype, d, n, sq):
+    b, hkv, hq, cap = 6, 2, 8, 2048
+    lengths = [0, 127, 128, 129, 1500, cap - n]
+    kc, vc = _nan_cache(b, hkv, cap, d, dtype, lengths, 9100)
+    nk = seeded((b, hkv, n, d), 9200, dtype=dtype)
+    nv = seeded((b, hkv, n, d), 9201, dtype=dtype)
+    q = seeded((b, hq, sq, d), 9202, dtype=dtype)
+    ek, ev = kc.clone(), vc.clone()
+    for i, s in enumerate(lengths):
+        ek[i, :, s:s + n] = nk[i]
+        ev[i, :, s:s + n] = nv[i]
+    seqlens = torch.tensor(lengths, device="cuda", dtype=torch.int32)
+    print(f"ragged append+decode dtype={dtype} d={d} n={n} sq={sq}", flush=True)
+    out, lse = attention_append_decode_ragged(q, kc, vc, nk, nv, seqlens, host_lengths=lengths,
+                                              scale=d ** -0.5, with_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(kc), _bits(ek)) and torch.equal(_bits(vc), _bits(ev))
+    tol = FWD_TOL[dtype]
+    for i, s in enumerate(lengths):
+        eo, el = reference_fp32(q[i:i + 1], ek[i:i + 1, :, :s + n], ev[i:i + 1, :, :s + n],
+                                causal=False)
+        assert_close(out[i:i + 1], eo, **tol, what=f"O seq {i} (L={s})")
+        assert_close(lse[i:i + 1], el, **tol, what=f"LSE seq {i} (L={s})")
+
+
+def test_ragged_append_decode_empty_cache_and_agrees_with_two_step_path():
+    """All lengths 0 (only the new tokens are visible), then a second call on
+    the grown cache compared with append + ragged decode on a copy."""
+    b, hkv, hq, cap, d, n = 2, 4, 16, 512, 64, 3
+    kc, vc = _nan_cache(b, hkv, cap, d, F16, [0, 0], 9300)
+    nk = seeded((b, hkv, n, d), 9301, dtype=F16)
+    nv = seeded((b, hkv, n, d), 9302, dtype=F16)
+    q = seeded((b, hq, n, d), 9303, dtype=F16)
+    seqlens = torch.zeros(b, device="cuda", dtype=torch.int32)
+    out = attention_append_decode_ragged(q, kc, vc, nk, nv, seqlens, host_lengths=[0, 0],
+                                         scale=0.125)
+    eo, _ = reference_fp32(q, nk, nv, causal=False)
+    assert_close(out, eo, **FWD_TOL[F16], what="O over new tokens only")
+    assert torch.equal(kc[:, :, :n], nk) and torch.equal(vc[:, :, :n], nv)
+    assert torch.isnan(kc[:, :, n:]).all() and torch.isnan(vc[:, :, n:]).all()
+
+    lengths = [n, n]
+    nk2 = seeded((b, hkv, 2, d), 9304, dtype=F16)
+    nv2 = seeded((b, hkv, 2, d), 9305, dtype=F16)
+    q2 = seeded((b, hq, 1, d), 9306, dtype=F16)
+    kc2, vc2 = kc.clone(), vc.clone()
+    seqlens.fill_(n)
+    fused = attention_append_decode_ragged(q2, kc, vc, nk2, nv2, seqlens,
+                                           host_lengths=lengths, scale=0.125)
+    kc2[:, :, n:n + 2] = nk2
+    vc2[:, :, n:n + 2] = nv2
+    seq2 = torch.full((b,), n + 2, device="cuda", dtype=torch.int32)
+    two_step = attention_decode_ragged(q2, kc2, vc2, seq2, max_seqlen=n + 2, scale=0.125)
+    assert torch.equal(_bits(kc), _bits(kc2)) and torch.equal(_bits(vc), _bits(vc2))
+    assert_close(fused, two_step, **FWD_TOL[F16], what="fused vs two-step")
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16])
+@pytest.mark.parametrize("past", [0, 1, 1023, 4095])
+def test_strided_append_scalar_position(dtype, past):
+    b, hkv, hq, cap, d = 2, 2, 8, 4096, 64
+    kc, vc = _nan_cache(b, hkv, cap, d, dtype, [past] * b, 9400)
+    nk = seeded((b, hkv, 1, d), 9401, dtype=dtype)
+    nv = seeded((b, hkv, 1, d), 9402, dtype=dtype)
+    q = seeded((b, hq, 1, d), 9403, dtype=dtype)
+    print(f"strided append dtype={dtype} past={past}", flush=True)
+    out = attention_forward_strided_append(q, kc, vc, nk, nv, past_length=past, scale=0.125)
+    torch.cuda.synchronize()
+    assert torch.equal(kc[:, :, past:past + 1], nk) and torch.equal(vc[:, :, past:past + 1], nv)
+    assert torch.isnan(kc[:, :, past + 1:]).all() and torch.isnan(vc[:, :, past + 1:]).all()
+    eo, _ = reference_fp32(q, kc[:, :, :past + 1], vc[:, :, :past + 1], causal=False)
+    assert_close(out, eo, **FWD_TOL[dtype], what=f"O past={past}")
+
+
+def test_ragged_cache_append_and_attend_fused_config5_steps():
+    """BASELINE config 5 shape for 6 steps through RaggedKVCache.append_and_attend
+    (auto = fused): cache [8, 8, 32768, 64] fp16, lengths U[4096, 28000],
+    n in [1, 16], Hq = 32 queries per new token."""
+    g = torch.Generator().manual_seed(501)
+    b, hkv, cap, d, hq = 8, 8, 32768, 64, 32
+    cache = RaggedKVCache(b, hkv, cap, d, device="cuda", dtype=F16)
+    cache.k.fill_(float("nan"))
+    cache.v.fill_(float("nan"))
+    lengths = torch.randint(4096, 28001, (b,), generator=g).tolist()
+    for i, n in enumerate(lengths):
+        cache.k[i, :, :n] = seeded((hkv, n, d), 530 + i, dtype=F16)
+        cache.v[i, :, :n] = seeded((hkv, n, d), 540 + i, dtype=F16)
+    cache.set_lengths(lengths)
+    for step in range(6):
+        n = int(torch.randint(1, 17, (1,), generator=g))
+        nk = seeded((b, hkv, n, d), 610 + step, dtype=F16)
+        nv = seeded((b, hkv, n, d), 710 + step, dtype=F16)
+        q = seeded((b, hq, n, d), 810 + step, dtype=F16)
+        before = list(cache.lengths)
+        with torch.inference_mode():
+            out = cache.append_and_attend(q, nk, nv)
+        assert cache.lengths == [x + n for x in before]
+        for i, s in enumerate(before):
+            assert torch.equal(cache.k[i, :, s:s + n], nk[i])
+            assert torch.equal(cache.v[i, :, s:s + n], nv[i])
+            assert torch.isnan(cache.k[i, :, s + n:s + n + 16]).all()
+        assert torch.isfinite(out).all()
+        for i in (0, step % b, b - 1):
+            kv, vv = cache.view(i)
+            eo, _ = reference_fp32(q[i:i + 1], kv, vv, causal=False)
+            assert_close(out[i:i + 1], eo, **FWD_TOL[F16], what=f"step {step} seq {i}")
