@@ -522,6 +522,9 @@ def main() -> int:
     ap.add_argument("--pmc-sample", action="store_true",
                     help="run one config 3 step plus a calibration fill/copy for rocprofv3 "
                          "--pmc and exit (prints no bench line)")
+    ap.add_argument("--only-config5", action="store_true",
+                    help="run only the config 5 append/decode loops (two-launch and fused) for "
+                         "a kernel trace and exit (prints no bench line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -545,6 +548,9 @@ def main() -> int:
     log(f"device: {torch.cuda.get_device_properties(0).gcnArchName}")
     if args.pmc_sample:
         log(json.dumps(pmc_sample(torch, _hip, dtype)))
+        return 0
+    if args.only_config5:
+        log(json.dumps(bench_config5(torch, _hip)))
         return 0
 
     ms, wall_ms, dkdv_live, per, work, step_flops = bench_train(torch, _hip, dtype, args.steps,

@@ -98,8 +98,23 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
   const int l16 = lane & 15, g16 = lane >> 4;
 
   int bid = blockIdx.x;
-  const int split = bid % p.nsplit;
-  bid /= p.nsplit;
+  int split;
+  if constexpr (APPEND) {
+    // The new tokens' workgroups (split nsplit - 1 of every row group) come
+    // first in the grid: they are short, and dispatched last they would end
+    // the launch.
+    const int ngrp = p.B * p.Hkv * p.nrb;
+    if (bid < ngrp) {
+      split = p.nsplit - 1;
+    } else {
+      bid -= ngrp;
+      split = bid % (p.nsplit - 1);
+      bid /= p.nsplit - 1;
+    }
+  } else {
+    split = bid % p.nsplit;
+    bid /= p.nsplit;
+  }
   const int rb = bid % p.nrb;
   bid /= p.nrb;
   const int kvh = bid % p.Hkv;

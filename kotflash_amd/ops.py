@@ -11,6 +11,9 @@ implementation and, for attention, a registered backward:
   K/V views read in place, inference only)
 - ``kotflash_amd::kv_append_(k_cache, v_cache, new_k, new_v, start) -> ()``
   (mutates both caches)
+- ``kotflash_amd::append_decode_(q, k_cache, v_cache, new_k, new_v,
+  past_length, scale) -> out`` (fused one-token append + split-KV decode,
+  reference kotflash/kernels/triton_decode.py:302-386; mutates both caches)
 
 ``torch.compile`` traces through them without graph breaks: the fake
 implementations give it output shapes, dtypes and strides, and autograd
@@ -24,10 +27,10 @@ from typing import Tuple
 import torch
 
 from .kernels.hip_backward import attention_backward
-from .kernels.hip_decode import attention_forward_strided_decode
+from .kernels.hip_decode import attention_forward_strided_append, attention_forward_strided_decode
 from .kernels.hip_forward import attention_forward
 
-__all__ = ["attn_fwd", "attn_bwd", "decode", "kv_append_"]
+__all__ = ["attn_fwd", "attn_bwd", "decode", "kv_append_", "append_decode_"]
 
 
 def _contig(t: torch.Tensor) -> torch.Tensor:
@@ -117,3 +120,19 @@ def kv_append_(k_cache: torch.Tensor, v_cache: torch.Tensor, new_k: torch.Tensor
 @kv_append_.register_fake
 def _kv_append_fake(k_cache, v_cache, new_k, new_v, start):
     return None
+
+
+@torch.library.custom_op("kotflash_amd::append_decode_", mutates_args=("k_cache", "v_cache"))
+def append_decode_(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                   new_k: torch.Tensor, new_v: torch.Tensor, past_length: int,
+                   scale: float) -> torch.Tensor:
+    """Store one new token at ``past_length`` of both caches and attend with
+    q [B, Hq, 1, D] over the first past_length + 1 positions (the split kernel
+    writes the token; two launches). Returns O."""
+    return _contig(attention_forward_strided_append(q, k_cache, v_cache, new_k, new_v,
+                                                    past_length=past_length, scale=scale))
+
+
+@append_decode_.register_fake
+def _append_decode_fake(q, k_cache, v_cache, new_k, new_v, past_length, scale):
+    return q.new_empty(q.shape)

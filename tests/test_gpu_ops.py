@@ -86,3 +86,18 @@ def test_kv_append_op_writes_only_the_slots():
     assert torch.isnan(vc[:, :, :30]).all() and torch.isnan(vc[:, :, 35:]).all()
     with pytest.raises(ValueError, match="capacity"):
         torch.ops.kotflash_amd.kv_append_(kc, vc, nk, nv, 60)
+
+
+def test_append_decode_op_writes_the_slot_and_attends():
+    kc = torch.full((2, 2, 2048, 64), float("nan"), dtype=F16, device="cuda")
+    vc = kc.clone()
+    kc[:, :, :1500] = seeded((2, 2, 1500, 64), 121, dtype=F16)
+    vc[:, :, :1500] = seeded((2, 2, 1500, 64), 122, dtype=F16)
+    nk = seeded((2, 2, 1, 64), 123, dtype=F16)
+    nv = seeded((2, 2, 1, 64), 124, dtype=F16)
+    q = seeded((2, 8, 1, 64), 125, dtype=F16)
+    out = torch.ops.kotflash_amd.append_decode_(q, kc, vc, nk, nv, 1500, 0.125)
+    assert torch.equal(kc[:, :, 1500:1501], nk) and torch.equal(vc[:, :, 1500:1501], nv)
+    assert torch.isnan(kc[:, :, 1501:]).all() and torch.isnan(vc[:, :, 1501:]).all()
+    eo, _ = reference_fp32(q, kc[:, :, :1501], vc[:, :, :1501], causal=False, scale=0.125)
+    assert_close(out, eo, **FWD_TOL[F16], what="append_decode_ O")

@@ -56,3 +56,15 @@ def test_kv_append_rejects_host_tensors():
     with pytest.raises(ValueError, match="requires GPU tensors"):
         torch.ops.kotflash_amd.kv_append_(cache, cache.clone(), new, new, 3)
     assert not cache.any()
+
+
+def test_append_decode_op_schema_and_fake():
+    sch = str(torch.ops.kotflash_amd.append_decode_.default._schema)
+    assert "Tensor(a1!) k_cache" in sch and "Tensor(a2!) v_cache" in sch
+    assert "Int past_length, float scale) -> Tensor" in sch
+    with FakeTensorMode():
+        q = torch.empty(2, 8, 1, 64, dtype=torch.float16)
+        kc = torch.empty(2, 2, 4096, 64, dtype=torch.float16)
+        new = torch.empty(2, 2, 1, 64, dtype=torch.float16)
+        out = torch.ops.kotflash_amd.append_decode_(q, kc, kc.clone(), new, new, 100, 0.125)
+        assert out.shape == q.shape and out.dtype == q.dtype
