@@ -148,3 +148,56 @@ def test_ragged_cache_append_and_attend_fused_config5_steps():
             kv, vv = cache.view(i)
             eo, _ = reference_fp32(q[i:i + 1], kv, vv, causal=False)
             assert_close(out[i:i + 1], eo, **FWD_TOL[F16], what=f"step {step} seq {i}")
+
+
+def test_fused_matches_oracle_append_then_split_merge():
+    """The fused call against the CPU oracle's own composition: kv_append
+    (kv_append_cuda.cu:12-40, per-sequence starts), then split-KV partials
+    over the post-append lengths and the LSE merge (triton_forward.py:
+    169-349). Cache bit-exact; O and LSE to fp16 tolerance."""
+    import numpy as np
+
+    from oracle import attention_oracle as orc
+
+    b, hkv, hq, cap, d, n = 3, 2, 8, 640, 64, 4
+    lengths = [0, 200, 500]
+    kc, vc = _nan_cache(b, hkv, cap, d, F16, lengths, 9500)
+    nk = seeded((b, hkv, n, d), 9501, dtype=F16)
+    nv = seeded((b, hkv, n, d), 9502, dtype=F16)
+    q = seeded((b, hq, n, d), 9503, dtype=F16)
+    ek, ev = kc.cpu().numpy(), vc.cpu().numpy()
+    orc.kv_append(ek, ev, nk.cpu().numpy(), nv.cpu().numpy(), lengths)
+    seqlens = torch.tensor(lengths, device="cuda", dtype=torch.int32)
+    out, lse = attention_append_decode_ragged(q, kc, vc, nk, nv, seqlens, host_lengths=lengths,
+                                              scale=0.125, with_lse=True)
+    assert kc.cpu().numpy().view(np.int16).tobytes() == ek.view(np.int16).tobytes()
+    assert vc.cpu().numpy().view(np.int16).tobytes() == ev.view(np.int16).tobytes()
+    after = [x + n for x in lengths]
+    po, pl = orc.split_kv_partials(q.cpu().numpy(), np.nan_to_num(ek), np.nan_to_num(ev),
+                                   scale=0.125, num_splits=3, chunk_n=256, seqlens=after)
+    eo, el = orc.split_kv_merge(po, pl)
+    assert_close(out, torch.from_numpy(eo), **FWD_TOL[F16], what="O vs oracle")
+    assert_close(lse, torch.from_numpy(el), **FWD_TOL[F16], what="LSE vs oracle")
+
+
+@pytest.mark.parametrize("n", [33, 200])
+def test_ragged_append_decode_many_new_tokens(n):
+    """More new tokens than one 32-key step: the new-token split streams
+    several steps over all four waves (keys 32 w + 128 j) before its copy."""
+    b, hkv, hq, cap, d = 3, 2, 4, 1024, 128
+    lengths = [0, 300, cap - n]
+    kc, vc = _nan_cache(b, hkv, cap, d, F16, lengths, 9600)
+    nk = seeded((b, hkv, n, d), 9601, dtype=F16)
+    nv = seeded((b, hkv, n, d), 9602, dtype=F16)
+    q = seeded((b, hq, 2, d), 9603, dtype=F16)
+    seqlens = torch.tensor(lengths, device="cuda", dtype=torch.int32)
+    print(f"ragged append+decode n={n}", flush=True)
+    out = attention_append_decode_ragged(q, kc, vc, nk, nv, seqlens, host_lengths=lengths,
+                                         scale=d ** -0.5)
+    torch.cuda.synchronize()
+    for i, s in enumerate(lengths):
+        assert torch.equal(kc[i, :, s:s + n], nk[i]) and torch.equal(vc[i, :, s:s + n], nv[i])
+        assert torch.isnan(kc[i, :, s + n:]).all() and torch.isnan(kc[i, :, :s]).logical_not().all()
+        eo, _ = reference_fp32(q[i:i + 1], kc[i:i + 1, :, :s + n], vc[i:i + 1, :, :s + n],
+                               causal=False)
+        assert_close(out[i:i + 1], eo, **FWD_TOL[F16], what=f"O seq {i} (L={s}, n={n})")
