@@ -18,16 +18,18 @@ def append_kv_hip(k_cache, v_cache, new_k, new_v, start: Union[int, torch.Tensor
     """Write new_k/new_v [B, H, S, D] into the caches [B, H, capacity, D] at
     positions start .. start+S-1 (``start`` an int, or a device int64 [B]
     tensor of per-sequence positions)."""
-    if not torch.cuda.is_available():
-        raise RuntimeError("a GPU is required for the kotflash_amd append kernel")
-    tensors = (k_cache, v_cache, new_k, new_v)
-    if any(not t.is_cuda for t in tensors):
+    # Written out check by check: this runs on every decode step, and
+    # generator expressions over the four tensors cost microseconds of host time.
+    if not (k_cache.is_cuda and v_cache.is_cuda and new_k.is_cuda and new_v.is_cuda):
         raise ValueError("all cache and source tensors must be GPU tensors")
-    if any(t.dtype not in (torch.float16, torch.bfloat16) for t in tensors):
+    dtype, ok = k_cache.dtype, (torch.float16, torch.bfloat16)
+    if (dtype not in ok or v_cache.dtype not in ok or new_k.dtype not in ok
+            or new_v.dtype not in ok):
         raise TypeError("the HIP append kernel supports FP16 and BF16 only")
-    if any(t.dtype != k_cache.dtype for t in tensors):
+    if v_cache.dtype != dtype or new_k.dtype != dtype or new_v.dtype != dtype:
         raise TypeError("all cache and source tensors must share one dtype")
-    if any(t.device != k_cache.device for t in tensors):
+    dev = k_cache.device
+    if v_cache.device != dev or new_k.device != dev or new_v.device != dev:
         raise ValueError("all cache and source tensors must be on the same GPU")
     if k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
         raise RuntimeError("K/V cache must have matching [B,H,capacity,D] shapes")

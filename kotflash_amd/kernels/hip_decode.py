@@ -99,7 +99,12 @@ def attention_forward_strided_append(q, k_cache, v_cache, new_k, new_v, *,
         raise ValueError("query, cache and new K/V shapes are incompatible")
     if hq % hkv or past_length < 0 or past_length + 1 > capacity:
         raise ValueError("unsupported head grouping, cache length or capacity")
-    if d % 8 == 0 and all(_hip.layout_ok(t) for t in (q, k_cache, v_cache)):
+    # The fused kernel addresses the whole cache (its store may land anywhere
+    # below the capacity) with 32-bit buffer offsets; the two-launch path
+    # only needs the visible prefix to fit.
+    fits = all(((capacity - 1) * t.stride(2) + d) * t.element_size() < 2 ** 31
+               for t in (k_cache, v_cache))
+    if d % 8 == 0 and fits and all(_hip.layout_ok(t) for t in (q, k_cache, v_cache)):
         new_k, new_v = (t if _hip.layout_ok(t) else t.contiguous() for t in (new_k, new_v))
         return _append_decode(q, k_cache, v_cache, new_k, new_v, None, past_length,
                               past_length, float(scale), with_lse=False)[0]
