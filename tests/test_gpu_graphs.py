@@ -112,3 +112,48 @@ def test_ragged_append_and_decode_graph_replays():
         for i, L in enumerate(lengths):
             assert torch.equal(kc[i, :, L:L + n], nk[i]) and torch.equal(vc[i, :, L:L + n], nv[i])
         assert bool(torch.isfinite(out).all())
+
+
+def test_fused_append_decode_graph_replays():
+    """kf_attn_append_decode captured in a graph: each replay stores the new
+    tokens (written eagerly before it) and decodes; every replay matches an
+    eager call on the same inputs bit for bit, cache included."""
+    b, hkv, hq, cap, d, n = 3, 2, 8, 4096, 64, 3
+    lengths = [0, 2900, 1400]
+    kc = torch.full((b, hkv, cap, d), float("nan"), dtype=F16, device="cuda")
+    vc = torch.full_like(kc, float("nan"))
+    for i, L in enumerate(lengths):
+        if L:
+            kc[i, :, :L] = seeded((hkv, L, d), 1900 + i, dtype=F16)
+            vc[i, :, :L] = seeded((hkv, L, d), 1910 + i, dtype=F16)
+    seqlens = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    nk = torch.empty((b, hkv, n, d), dtype=F16, device="cuda")
+    nv = torch.empty_like(nk)
+    q = torch.empty((b, hq, n, d), dtype=F16, device="cuda")
+    out = torch.empty_like(q)
+    lse = torch.empty((b, hq, n), dtype=torch.float32, device="cuda")
+    splits = _hip.decode_num_splits_ragged(b, hq, hkv, n, lengths, d)
+    ws = torch.empty(_hip.decode_workspace_bytes(b, hq, hkv, n, d, splits + 1),
+                     dtype=torch.uint8, device="cuda")
+
+    def step():
+        _hip.append_decode(q, kc, vc, nk, nv, out, lse, seqlens, past_length=0,
+                           max_length=max(lengths), scale=0.125, num_splits=splits, workspace=ws)
+
+    for t, seed in zip((nk, nv, q), (1921, 1922, 1923)):
+        t.copy_(seeded(t.shape, seed, dtype=F16))
+    graph, _ = _capture(step)
+    for r in range(3):
+        for t, seed in zip((nk, nv, q), (1930, 1940, 1950)):
+            t.copy_(seeded(t.shape, seed + r, dtype=F16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got, got_lse = out.clone(), lse.clone()
+        for i, L in enumerate(lengths):
+            assert torch.equal(kc[i, :, L:L + n], nk[i]) and torch.equal(vc[i, :, L:L + n], nv[i])
+            assert torch.isnan(kc[i, :, L + n:]).all()
+        step()
+        torch.cuda.synchronize()
+        assert torch.equal(got, out) and torch.equal(got_lse, lse), f"replay {r}"
+        assert bool(torch.isfinite(out).all())
