@@ -81,6 +81,27 @@ def decode_step(q_new, k_cache, v_cache, k_new, v_new, *, backend: str = "auto")
     return output, updated_k, updated_v
 
 
+def _auto_fuses(q: torch.Tensor, cache: torch.Tensor, visible: int, attention_backend: str,
+                has_grad: bool) -> bool:
+    """Whether ``append_backend="auto"`` takes the fused append + decode: the
+    native append is enabled (``_use_hip_append``), there is no autograd, the
+    head_dim is a multiple of 8, and the attention backend is the HIP one --
+    forced, or ``auto`` routing this decode shape (``visible`` keys after the
+    append) to it."""
+    if has_grad or attention_backend not in ("auto", "hip", "triton") or q.shape[-1] % 8:
+        return False
+    if not _use_hip_append("auto", cache):
+        return False
+    if attention_backend != "auto":
+        return True
+    from ._planning import gfx950_profile_for_shapes
+
+    k_shape = (cache.shape[0], cache.shape[1], visible, cache.shape[3])
+    dtype_name = str(q.dtype).replace("torch.", "")
+    return gfx950_profile_for_shapes(tuple(q.shape), k_shape, causal=False,
+                                     dtype_name=dtype_name) == "hip"
+
+
 def _use_hip_append(backend: str, cache: torch.Tensor) -> bool:
     if backend in ("hip", "cuda"):
         return True
@@ -177,8 +198,10 @@ class PreallocatedKVCache:
         prefix (reference cache.py:191-277).
 
         ``append_backend="fused"`` runs the inference-only append + decode
-        launcher (one append launch and the split-KV decode); it needs an
-        explicit or automatic HIP attention backend and no autograd.
+        launcher (the split-KV kernel also stores the token, then the merge);
+        it needs an explicit or automatic HIP attention backend and no
+        autograd. ``"auto"`` takes it whenever it applies (``_auto_fuses``),
+        else appends with the HIP kernel or torch copies and attends.
         """
         if attention_backend not in ("auto", "hip", "triton", "sdpa"):
             raise ValueError("attention backend must be one of: auto, hip, triton or sdpa")
@@ -196,7 +219,8 @@ class PreallocatedKVCache:
         has_grad = torch.is_grad_enabled() and any(
             t.requires_grad for t in (q_new, new_k, new_v)
         )
-        if append_backend == "fused":
+        if append_backend == "fused" or (append_backend == "auto" and _auto_fuses(
+                q_new, self.k, end, attention_backend, has_grad)):
             if attention_backend == "sdpa":
                 raise ValueError("append_backend='fused' requires attention_backend='auto' or 'hip'")
             if has_grad:
@@ -285,10 +309,9 @@ class RaggedKVCache(PreallocatedKVCache):
 
         ``append_backend="fused"`` stores the new tokens from inside the
         split-KV decode (one decode launch and the merge, no append launch;
-        inference only). ``"auto"`` takes it when the HIP decode applies
-        (gfx950, fp16/bf16, head_dim a multiple of 8, no autograd) and
-        ``attention_backend`` is "auto" or "hip"; otherwise it appends
-        (``append``) and attends (``attend``) as two steps.
+        inference only). ``"auto"`` takes it when it applies (``_auto_fuses``);
+        otherwise it appends (``append``) and attends (``attend``) as two
+        steps.
         """
         if attention_backend not in ("auto", "hip", "triton", "sdpa"):
             raise ValueError("attention backend must be one of: auto, hip, triton or sdpa")
@@ -314,12 +337,8 @@ class RaggedKVCache(PreallocatedKVCache):
         has_grad = torch.is_grad_enabled() and any(
             t.requires_grad for t in (q_new, new_k, new_v)
         )
-        fusable = (q_new.is_cuda and q_new.dtype in (torch.float16, torch.bfloat16)
-                   and q_new.shape[-1] % 8 == 0 and _hip.is_gfx950(q_new.device)
-                   and _hip.library_available())
-        fused = append_backend == "fused" or (
-            append_backend == "auto" and fusable and not has_grad
-            and attention_backend in ("auto", "hip", "triton"))
+        fused = append_backend == "fused" or (append_backend == "auto" and _auto_fuses(
+            q_new, self.k, max(self.lengths) + n, attention_backend, has_grad))
         if fused:
             if attention_backend == "sdpa":
                 raise ValueError("append_backend='fused' requires attention_backend='auto' or 'hip'")

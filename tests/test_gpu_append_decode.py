@@ -201,3 +201,43 @@ def test_ragged_append_decode_many_new_tokens(n):
         eo, _ = reference_fp32(q[i:i + 1], kc[i:i + 1, :, :s + n], vc[i:i + 1, :, :s + n],
                                causal=False)
         assert_close(out[i:i + 1], eo, **FWD_TOL[F16], what=f"O seq {i} (L={s}, n={n})")
+
+
+def test_preallocated_cache_auto_takes_fused_path_when_it_applies(monkeypatch):
+    """PreallocatedKVCache.append_and_attend with the default backends fuses
+    the append into the decode for an inference-only decode shape, and keeps
+    the two-step path with autograd or below the decode envelope."""
+    from kotflash_amd.cache import PreallocatedKVCache
+    import kotflash_amd.kernels.hip_decode as hd
+
+    calls = []
+    real = hd.attention_forward_strided_append
+
+    def counting(*args, **kwargs):
+        calls.append(kwargs["past_length"])
+        return real(*args, **kwargs)
+
+    monkeypatch.setattr(hd, "attention_forward_strided_append", counting)
+    cache = PreallocatedKVCache(2, 2, 4096, 64, device="cuda", dtype=F16)
+    cache.k.fill_(float("nan"))
+    cache.v.fill_(float("nan"))
+    pk, pv = seeded((2, 2, 2047, 64), 9701, dtype=F16), seeded((2, 2, 2047, 64), 9702, dtype=F16)
+    cache.append(pk, pv, backend="torch")
+    nk, nv = seeded((2, 2, 1, 64), 9703, dtype=F16), seeded((2, 2, 1, 64), 9704, dtype=F16)
+    q = seeded((2, 8, 1, 64), 9705, dtype=F16)
+    with torch.inference_mode():
+        out = cache.append_and_attend(q, nk, nv)
+    assert calls == [2047] and cache.length == 2048
+    assert torch.equal(cache.k[:, :, 2047:2048], nk) and torch.isnan(cache.k[:, :, 2048:]).all()
+    eo, _ = reference_fp32(q, torch.cat((pk, nk), 2), torch.cat((pv, nv), 2), causal=False)
+    assert_close(out, eo, **FWD_TOL[F16], what="auto (fused) O")
+    # Autograd: the two-step path.
+    qg = q.clone().requires_grad_(True)
+    out2 = cache.append_and_attend(qg, nk, nv)
+    assert calls == [2047] and cache.length == 2049 and out2.requires_grad
+    # Below the split-KV decode envelope (auto attention goes to SDPA): two-step.
+    small = PreallocatedKVCache(2, 2, 256, 64, device="cuda", dtype=F16)
+    small.append(pk[:, :, :100], pv[:, :, :100], backend="torch")
+    with torch.inference_mode():
+        small.append_and_attend(q, nk, nv)
+    assert calls == [2047] and small.length == 101
