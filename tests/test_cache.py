@@ -197,3 +197,25 @@ def test_ragged_cache_append_and_attend_two_step_path_on_cpu():
                                 attention_backend="sdpa")
     with pytest.raises(ValueError, match="append backend"):
         cache.append_and_attend(q, nk, nv, append_backend="nope")
+
+
+def test_auto_fuses_routing(monkeypatch):
+    """append_backend='auto' picks the fused append + decode only for
+    inference-only calls whose attention goes to the HIP decode; the native
+    append check (_use_hip_append) is patched in, so this runs on the CPU."""
+    from kotflash_amd import cache as cache_mod
+
+    monkeypatch.setattr(cache_mod, "_use_hip_append", lambda backend, t: True)
+    kc = torch.empty(2, 2, 8, 64, dtype=torch.float16)
+    q = torch.empty(2, 8, 1, 64, dtype=torch.float16)
+    fuses = cache_mod._auto_fuses
+    assert fuses(q, kc, 4096, "auto", False)            # split-KV decode shape
+    assert not fuses(q, kc, 100, "auto", False)         # auto attention -> SDPA
+    assert fuses(q, kc, 100, "hip", False)              # HIP forced
+    assert not fuses(q, kc, 4096, "sdpa", False)
+    assert not fuses(q, kc, 4096, "auto", True)         # autograd
+    q72 = torch.empty(2, 8, 1, 12, dtype=torch.float16)
+    assert not fuses(q72, torch.empty(2, 2, 8, 12, dtype=torch.float16), 4096, "hip", False)
+    assert not fuses(q.float(), kc.float(), 4096, "auto", False)  # fp32: SDPA
+    monkeypatch.setattr(cache_mod, "_use_hip_append", lambda backend, t: False)
+    assert not fuses(q, kc, 4096, "hip", False)         # native append disabled
