@@ -852,18 +852,19 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
 }
 
 // ---------------------------------------------------------------------------
-// 4. Fixup: kFixSub workgroups per key tile, 16 keys each. Sums the partials
+// 4. Fixup: kFixSub workgroups per key tile, kFixKeys keys each. Sums the partials
 // of tiles shared by several dkdv workgroups, zero-fills tiles that no query
 // can see, and leaves tiles one workgroup finished alone untouched.
-constexpr int kFixSub = kBNK / 16;
+constexpr int kFixKeys = 16;  // keys per fixup workgroup
+constexpr int kFixSub = kBNK / kFixKeys;
 template <typename T, int DT, bool CAUSAL>
 __global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p, const DkdvSplit sp) {
   const int t = blockIdx.x / kFixSub, sub = blockIdx.x % kFixSub;
   const int kt = t / p.ngroups, grp = t % p.ngroups;
   const int b = grp / p.Hkv, kvh = grp % p.Hkv;
-  const int k0 = kt * kBNK + sub * 16;
+  const int k0 = kt * kBNK + sub * kFixKeys;
   const int nq = dkdv_nq(kt, p.nqt, CAUSAL);
-  const int nkeys = min(16, p.Sk - k0);
+  const int nkeys = min(kFixKeys, p.Sk - k0);
   if (nkeys <= 0) return;
   constexpr int QPR = DT / 4;
   if (nq == 0) {
@@ -882,7 +883,7 @@ __global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p, cons
   const int w0 = dkdv_owner(sp, p.nwg, first), w1 = dkdv_owner(sp, p.nwg, last);
   if (w0 == w1) return;
   for (int e = threadIdx.x; e < nkeys * QPR; e += 256) {
-    const int kr = sub * 16 + e / QPR, d = (e % QPR) * 4;
+    const int kr = sub * kFixKeys + e / QPR, d = (e % QPR) * 4;
     if (d >= p.D) continue;
     float4 sk = make_float4(0.f, 0.f, 0.f, 0.f), sv = sk;
     for (int w = w0; w <= w1; ++w) {
