@@ -171,9 +171,8 @@ class _DeviceGuard:
 def layout_ok(t: torch.Tensor) -> bool:
     """Whether the kernels can read ``t`` in place: unit head_dim stride,
     other strides multiples of 8 elements, 16-byte aligned base."""
-    if t.ndim != 4 or t.stride(3) != 1:
-        return False
-    if any(s % 8 for s in t.stride()[:3]):
+    s = t.stride()
+    if len(s) != 4 or s[3] != 1 or s[0] % 8 or s[1] % 8 or s[2] % 8:
         return False
     return t.data_ptr() % 16 == 0
 

@@ -20,7 +20,7 @@ import torch.nn.functional as F
 from . import _hip
 from ._planning import gfx950_profile_for_shapes, t4_profile_for_shapes
 from .kernels.hip_backward import attention_backward
-from .kernels.hip_decode import attention_forward_strided_decode, strided_decode_supported
+from .kernels.hip_decode import decode_supported_unchecked, strided_decode_supported
 from .kernels.hip_forward import attention_forward, triton_turing_supported
 
 BACKENDS = ("auto", "hip", "triton", "sdpa")
@@ -279,7 +279,7 @@ def attention(
     if (explicit or route == "hip") and not causal and strided_decode_supported(q, k, v):
         needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
         if not needs_grad:
-            return attention_forward_strided_decode(q, k, v, scale=float(scale))
+            return decode_supported_unchecked(q, k, v, float(scale))
 
     if explicit:
         if not hip_supported(q, k):

@@ -30,16 +30,21 @@ def unpad(t: torch.Tensor, d: int) -> torch.Tensor:
 
 def require_hip_tensors(what: str, *tensors: torch.Tensor) -> None:
     """Fail loudly (no fallback) when the HIP path cannot run these tensors."""
-    if not all(t.is_cuda for t in tensors):
-        raise ValueError(f"{what} requires GPU tensors")
+    # Plain loops: this runs on every decode call, where generator
+    # expressions cost measurable host time.
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError(f"{what} requires GPU tensors")
     dtype = tensors[0].dtype
     if dtype not in (torch.float16, torch.bfloat16):
         raise TypeError(f"{what} supports float16 and bfloat16 only")
-    if any(t.dtype != dtype for t in tensors):
-        raise TypeError(f"{what}: all tensors must share one dtype")
+    for t in tensors:
+        if t.dtype != dtype:
+            raise TypeError(f"{what}: all tensors must share one dtype")
     dev = tensors[0].device
-    if any(t.device != dev for t in tensors):
-        raise ValueError(f"{what}: all tensors must be on the same device")
+    for t in tensors:
+        if t.device != dev:
+            raise ValueError(f"{what}: all tensors must be on the same device")
     if not _hip.is_gfx950(dev):
         raise RuntimeError(f"{what} requires an AMD gfx950 (MI355X) device")
     _hip.lib()  # raises RuntimeError when the library is missing

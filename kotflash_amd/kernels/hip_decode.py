@@ -25,22 +25,24 @@ def strided_decode_supported(q, k, v) -> bool:
     head_dim stride, 8-element multiple strides and 16-byte alignment -- which
     includes the padded prefix views of ``PreallocatedKVCache`` (reference
     triton_decode.py:389-409 accepts only D <= 64 and fp16)."""
-    if not all(isinstance(t, torch.Tensor) for t in (q, k, v)):
+    if not (isinstance(q, torch.Tensor) and isinstance(k, torch.Tensor)
+            and isinstance(v, torch.Tensor)):
         return False
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         return False
     if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
         return False
-    if q.ndim != 4 or k.ndim != 4 or v.shape != k.shape:
+    qs, ks = q.shape, k.shape
+    if len(qs) != 4 or len(ks) != 4 or v.shape != ks:
         return False
-    if q.shape[0] != k.shape[0] or q.shape[1] % k.shape[1] or q.shape[3] != k.shape[3]:
+    if qs[0] != ks[0] or qs[1] % ks[1] or qs[3] != ks[3]:
         return False
-    d = q.shape[3]
-    if q.shape[2] > GFX950_DECODE_MAX_SQ or k.shape[2] < GFX950_DECODE_MIN_SK:
+    d = qs[3]
+    if qs[2] > GFX950_DECODE_MAX_SQ or ks[2] < GFX950_DECODE_MIN_SK:
         return False
     if not gfx950_head_dim_ok(d) or d % 8:
         return False
-    if not all(_hip.layout_ok(t) for t in (q, k, v)):
+    if not (_hip.layout_ok(q) and _hip.layout_ok(k) and _hip.layout_ok(v)):
         return False
     return _hip.is_gfx950(q.device) and _hip.library_available()
 
@@ -69,6 +71,13 @@ def attention_forward_strided_decode(q, k, v, *, scale: float):
             "expected fp16/bf16 gfx950 tensors with a short query, a long key "
             "sequence and an inner-contiguous, 16-byte aligned K/V layout"
         )
+    return _decode(q, k, v, None, float(scale), with_lse=False)[0]
+
+
+def decode_supported_unchecked(q, k, v, scale: float):
+    """``attention_forward_strided_decode`` for a caller that has just
+    checked ``strided_decode_supported(q, k, v)`` (the public ``attention``),
+    without checking again."""
     return _decode(q, k, v, None, float(scale), with_lse=False)[0]
 
 
@@ -102,10 +111,14 @@ def attention_forward_strided_append(q, k_cache, v_cache, new_k, new_v, *,
     # The fused kernel addresses the whole cache (its store may land anywhere
     # below the capacity) with 32-bit buffer offsets; the two-launch path
     # only needs the visible prefix to fit.
-    fits = all(((capacity - 1) * t.stride(2) + d) * t.element_size() < 2 ** 31
-               for t in (k_cache, v_cache))
-    if d % 8 == 0 and fits and all(_hip.layout_ok(t) for t in (q, k_cache, v_cache)):
-        new_k, new_v = (t if _hip.layout_ok(t) else t.contiguous() for t in (new_k, new_v))
+    fits = (((capacity - 1) * k_cache.stride(2) + d) * 2 < 2 ** 31
+            and ((capacity - 1) * v_cache.stride(2) + d) * 2 < 2 ** 31)
+    if (d % 8 == 0 and fits and _hip.layout_ok(q) and _hip.layout_ok(k_cache)
+            and _hip.layout_ok(v_cache)):
+        if not _hip.layout_ok(new_k):
+            new_k = new_k.contiguous()
+        if not _hip.layout_ok(new_v):
+            new_v = new_v.contiguous()
         return _append_decode(q, k_cache, v_cache, new_k, new_v, None, past_length,
                               past_length, float(scale), with_lse=False)[0]
     _hip.kv_append(k_cache, v_cache, new_k, new_v, start=past_length)
