@@ -528,7 +528,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(see DESIGN.md for how the path would shard)", file=sys.stderr)
+              "(the path shards over independent (batch, kv_head) groups with no exchange; "
+              "one GPU runs one shard's shape)", file=sys.stderr)
         return 2
     if args.steps < 1 or args.warmup < 0:
         print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
