@@ -122,15 +122,6 @@ def _t4_profile_backend(q, k, v, *, causal: bool, scale: float):
     )
 
 
-def _t4_auto_strided_decode_profile(q, k, v, *, causal: bool, scale: float) -> bool:
-    """The reference's exact-shape strided decode gate (attention.py:108-117)."""
-    if causal or not math.isclose(scale, 0.125, rel_tol=0.0, abs_tol=1e-12):
-        return False
-    if tuple(q.shape) != (2, 8, 1, 64) or tuple(k.shape) != (2, 2, 2048, 64):
-        return False
-    return _is_measured_t4_runtime(_device_index(q)) and strided_decode_supported(q, k, v)
-
-
 def _gfx950_profile_backend(q, k, v, *, causal: bool):
     """``"hip"`` when ``auto`` should use the HIP kernels on this device."""
     if not q.is_cuda or not _hip.is_gfx950(q.device):
