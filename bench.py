@@ -69,7 +69,33 @@ def seeded(torch, shape, seed, dtype, scale=1.0, device="cuda"):
     return (torch.randn(*shape, generator=g) * scale).to(dtype).to(device)
 
 
-def bench_train(torch, _hip, dtype, steps, warmup, cfg=None, causal=True, qkv_scale=0.5):
+# An idle MI355X raises its clocks over the first ~30 ms of MFMA load: from a
+# cold start the config 3 step measured 3.47 ms (first launch), then 0.68 to
+# 0.86 ms over steps 1-20 and a steady 0.665 ms from step ~40 on. Steps of a
+# training loop run back to back, so the figure is taken at the steady
+# state: untimed steps run for PREWARM_MS of wall time before the --warmup
+# steps, and the JSON line states how many.
+PREWARM_MS = 200.0
+
+
+def prewarm(torch, fn, ms):
+    """Run ``fn`` untimed until ``ms`` milliseconds of wall time have passed
+    (checked every 10 calls, after a synchronize); returns the call count."""
+    if ms <= 0:
+        return 0
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(10):
+            fn()
+        n += 10
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= ms:
+            return n
+
+
+def bench_train(torch, _hip, dtype, steps, warmup, cfg=None, causal=True, qkv_scale=0.5,
+                prewarm_ms=PREWARM_MS):
     c = cfg or CFG3
     b, hq, hkv, s, d = c["B"], c["Hq"], c["Hkv"], c["S"], c["D"]
     scale = 1.0 / math.sqrt(d)
@@ -108,6 +134,7 @@ def bench_train(torch, _hip, dtype, steps, warmup, cfg=None, causal=True, qkv_sc
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for e in [start, stop] + [x for pair in evs for x in pair]:
         e.record()
+    nwarm = prewarm(torch, step, prewarm_ms)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -142,7 +169,7 @@ def bench_train(torch, _hip, dtype, steps, warmup, cfg=None, causal=True, qkv_sc
     }
     f = fwd_flops(b, hq, s, d) if causal else 4.0 * d * b * hq * s * s
     work = {"attn_fwd": f, "bwd_dq": 0.5 * f, "bwd_dkdv": 2.0 * f, "bwd_dkdv_fixup": 0.0}
-    return ms, wall_ms, dkdv_live, per, work, 3.5 * f
+    return ms, wall_ms, dkdv_live, per, work, 3.5 * f, nwarm
 
 
 def pmc_sample(torch, _hip, dtype):
@@ -398,12 +425,12 @@ def side_configs(torch, _hip, steps):
         r = bench_decode(torch, _hip, torch.float16, sk)
         res["config2_decode_sweep"][str(sk)] = {k: r[k] for k in
                                                 ("us_per_call", "hbm_gbps", "hbm_frac", "num_splits")}
-    ms, _, _, per, work, flops = bench_train(torch, _hip, torch.bfloat16, steps, steps // 2)
+    ms, _, _, per, work, flops, _ = bench_train(torch, _hip, torch.bfloat16, steps, steps // 2)
     res["config3_bf16"] = {"ms_per_step": ms, "tflops": flops / (ms * 1e-3) / 1e12,
                            "frac": flops / (ms * 1e-3) / PEAK_MFMA_F16}
     for dd in (72, 96):
         c4 = dict(B=4, Hq=12, Hkv=12, S=2048, D=dd)
-        ms, _, _, per, work, flops = bench_train(torch, _hip, torch.float16, steps, steps // 2, c4,
+        ms, _, _, per, work, flops, _ = bench_train(torch, _hip, torch.float16, steps, steps // 2, c4,
                                                  causal=False, qkv_scale=1.0)
         res[f"config4_d{dd}"] = {
             "workload": f"BASELINE config 4: non-causal MHA fwd+bwd B=4 H=12 S=2048 D={dd} fp16",
@@ -514,6 +541,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100,
                     help="untimed steps first; ~0.1 s of work lets the GPU clocks settle")
+    ap.add_argument("--prewarm-ms", type=float, default=PREWARM_MS,
+                    help="untimed steps for this much wall time before the --warmup steps "
+                         "(GPU clock ramp); reported in the JSON line")
     ap.add_argument("--dtype", choices=("float16", "bfloat16"), default="float16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
@@ -554,8 +584,8 @@ def main() -> int:
         log(json.dumps(bench_config5(torch, _hip)))
         return 0
 
-    ms, wall_ms, dkdv_live, per, work, step_flops = bench_train(torch, _hip, dtype, args.steps,
-                                                                args.warmup)
+    ms, wall_ms, dkdv_live, per, work, step_flops, prewarm_steps = bench_train(
+        torch, _hip, dtype, args.steps, args.warmup, prewarm_ms=args.prewarm_ms)
     log(f"train step: {ms:.4f} ms (GPU events), {wall_ms:.4f} ms (wall); dkdv live "
         f"{dkdv_live:.4f} ms; isolated per kernel {per}")
     api_ms = bench_api(torch, kf, dtype, max(5, args.steps // 5), 2)
@@ -587,6 +617,9 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "prewarm": {"ms": args.prewarm_ms, "steps": prewarm_steps,
+                    "why": "untimed steps before the --warmup steps while the GPU clocks ramp "
+                           "(~30 ms of load from idle)"},
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",

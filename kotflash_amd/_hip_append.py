@@ -7,17 +7,25 @@ accepted, and ``start`` may be a per-sequence device tensor.
 """
 from __future__ import annotations
 
-from typing import Union
+from typing import Optional, Sequence, Union
 
 import torch
 
 from . import _hip
 
 
-def append_kv_hip(k_cache, v_cache, new_k, new_v, start: Union[int, torch.Tensor]) -> None:
+def append_kv_hip(k_cache, v_cache, new_k, new_v, start: Union[int, torch.Tensor], *,
+                  host_starts: Optional[Sequence[int]] = None) -> None:
     """Write new_k/new_v [B, H, S, D] into the caches [B, H, capacity, D] at
     positions start .. start+S-1 (``start`` an int, or a device int64 [B]
-    tensor of per-sequence positions)."""
+    tensor of per-sequence positions).
+
+    Every position is range-checked before anything is written, as the
+    reference's op does (kv_append_cuda.cu:50-75): an append that would leave
+    [0, capacity) raises RuntimeError and the caches stay unchanged. For a
+    device ``start`` tensor the check uses ``host_starts`` (the same positions
+    on the host, e.g. a cache's own length mirror) when given, and otherwise
+    copies ``start`` to the host, which synchronizes with the device."""
     # Written out check by check: this runs on every decode step, and
     # generator expressions over the four tensors cost microseconds of host time.
     if not (k_cache.is_cuda and v_cache.is_cuda and new_k.is_cuda and new_v.is_cuda):
@@ -47,6 +55,17 @@ def append_kv_hip(k_cache, v_cache, new_k, new_v, start: Union[int, torch.Tensor
     if isinstance(start, torch.Tensor):
         if start.dtype != torch.int64 or start.device != k_cache.device or start.shape != (new_k.shape[0],):
             raise ValueError("per-sequence start must be a device int64 tensor of shape [B]")
+        # The kernel reads start[b] as a dense array: an expanded or strided
+        # view is materialised first.
+        if not start.is_contiguous():
+            start = start.contiguous()
+        starts = start.tolist() if host_starts is None else host_starts
+        if len(starts) != new_k.shape[0]:
+            raise ValueError("host_starts must have one entry per batch element")
+        n, capacity = new_k.shape[2], k_cache.shape[2]
+        for s in starts:
+            if s < 0 or s + n > capacity:
+                raise RuntimeError("append range exceeds cache capacity")
         _hip.kv_append(k_cache, v_cache, new_k, new_v, start_dev=start)
     else:
         start = int(start)

@@ -106,15 +106,17 @@ def gfx950_decode_eligible(sq: int, sk: int, d: int, *, causal: bool) -> bool:
             and gfx950_head_dim_ok(d))
 
 
-# Below this much forward work (FLOP) an eager call is bound by host time, and
-# PyTorch's SDPA, whose launch path is C++, finishes first. Measured on MI355X
+# Below this much forward work (FLOP) an eager training call (forward, then
+# backward through autograd) is bound by host time, and PyTorch's SDPA,
+# whose launch and autograd paths are C++, finishes first. Measured on MI355X
 # through the public API (python -m kotflash_amd.benchmark, B=2 Hq=8 Hkv=2
-# D=64 causal, fp16; fwd / fwd+bwd us, HIP vs SDPA):
-#   S=256: 29.6/253 vs 27.3/188;  S=512: 29.8/243 vs 26.5/185;
-#   S=1024: 30.6/248 vs 36.6/263;  S=2048: 30.2/261 vs 57.5/411;
-#   and B=1 H=8 S=512 D=128 non-causal (1.1e9 FLOP): 32.3/250 vs 23.9/175.
-# Split-KV decode shapes are not subject to it (HIP decode is 14x faster at
-# config 2).
+# D=64 causal, fp16; fwd+bwd us, HIP vs SDPA):
+#   S=256: 253 vs 188;  S=512: 243 vs 185;  S=1024: 248 vs 263;
+#   S=2048: 261 vs 411;  B=1 H=8 S=512 D=128 non-causal (1.1e9 FLOP): 250 vs 175.
+# Inference calls (no backward to follow) are not subject to it: the HIP
+# forward's launch path is the shorter one (config 1, S=512: 18.9 us per call
+# against 22.4 us for SDPA, bench.py torch_sdpa_same_gpu), and split-KV decode
+# shapes are 22x faster (config 2).
 GFX950_HIP_MIN_FWD_FLOPS = 1.5e9
 
 
@@ -133,13 +135,15 @@ def attention_fwd_flops(q_shape: Sequence[int], k_shape: Sequence[int], *, causa
 
 def gfx950_profile_for_shapes(
     q_shape: Sequence[int], k_shape: Sequence[int], *, causal: bool, dtype_name: str,
+    needs_grad: bool = True,
 ) -> Optional[str]:
     """Backend chosen by ``backend="auto"`` on gfx950, else None (SDPA).
 
     The HIP kernels cover fp16/bf16 with 8 <= head_dim <= 128 for any
-    sequence lengths and GQA grouping. ``auto`` takes them for split-KV decode
-    shapes and for problems of at least ``GFX950_HIP_MIN_FWD_FLOPS``; smaller
-    ones, and everything outside that envelope, go to SDPA.
+    sequence lengths and GQA grouping. ``auto`` takes them for every
+    inference call (``needs_grad=False``), for split-KV decode shapes, and for
+    training calls of at least ``GFX950_HIP_MIN_FWD_FLOPS``; smaller training
+    calls, and everything outside that envelope, go to SDPA.
     """
     if dtype_name not in ("float16", "bfloat16"):
         return None
@@ -150,7 +154,7 @@ def gfx950_profile_for_shapes(
         return None
     if q_shape[1] % k_shape[1] != 0:
         return None
-    if gfx950_decode_eligible(q_shape[2], k_shape[2], d, causal=causal):
+    if not needs_grad or gfx950_decode_eligible(q_shape[2], k_shape[2], d, causal=causal):
         return "hip"
     if attention_fwd_flops(q_shape, k_shape, causal=causal) < GFX950_HIP_MIN_FWD_FLOPS:
         return None

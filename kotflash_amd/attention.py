@@ -122,12 +122,13 @@ def _t4_profile_backend(q, k, v, *, causal: bool, scale: float):
     )
 
 
-def _gfx950_profile_backend(q, k, v, *, causal: bool):
+def _gfx950_profile_backend(q, k, v, *, causal: bool, needs_grad: bool = True):
     """``"hip"`` when ``auto`` should use the HIP kernels on this device."""
     if not q.is_cuda or not _hip.is_gfx950(q.device):
         return None
     route = gfx950_profile_for_shapes(
         q.shape, k.shape, causal=causal, dtype_name=_DTYPE_NAMES.get(q.dtype, ""),
+        needs_grad=needs_grad,
     )
     if route == "hip" and not _hip.library_available():
         # A gfx950 device without the library is a broken install, not an
@@ -243,8 +244,11 @@ def attention(
     RuntimeError otherwise. For non-causal short queries (Sq <= 16) against
     long caches (Sk >= 1024) without autograd, the HIP path reads K/V in place
     (padded ``PreallocatedKVCache`` views included) with split-KV decode; the
-    caller must pass only keys visible to every query. auto uses the HIP
-    kernels for fp16/bf16 on gfx950 and SDPA everywhere else.
+    caller must pass only keys visible to every query. On gfx950, auto uses
+    the HIP kernels for fp16/bf16 inference calls and decode shapes, and for
+    training calls (autograd) of at least 1.5e9 forward FLOP, below which an
+    eager training step is host-bound and SDPA finishes first; SDPA
+    everywhere else.
     """
     _validate(q, k, v)
     if not isinstance(causal, bool):
@@ -262,15 +266,16 @@ def attention(
         raise ValueError("backend must be one of: auto, hip, triton, sdpa")
 
     explicit = backend in ("hip", "triton")
+    needs_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad
+                                              or v.requires_grad)
     route = None
     if backend == "auto":
-        route = _gfx950_profile_backend(q, k, v, causal=causal)
+        route = _gfx950_profile_backend(q, k, v, causal=causal, needs_grad=needs_grad)
 
     # Inference on preallocated caches: read the (padded) K/V views in place.
-    if (explicit or route == "hip") and not causal and strided_decode_supported(q, k, v):
-        needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
-        if not needs_grad:
-            return decode_supported_unchecked(q, k, v, float(scale))
+    if (explicit or route == "hip") and not causal and not needs_grad \
+            and strided_decode_supported(q, k, v):
+        return decode_supported_unchecked(q, k, v, float(scale))
 
     if explicit:
         if not hip_supported(q, k):

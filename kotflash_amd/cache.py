@@ -99,7 +99,7 @@ def _auto_fuses(q: torch.Tensor, cache: torch.Tensor, visible: int, attention_ba
     k_shape = (cache.shape[0], cache.shape[1], visible, cache.shape[3])
     dtype_name = str(q.dtype).replace("torch.", "")
     return gfx950_profile_for_shapes(tuple(q.shape), k_shape, causal=False,
-                                     dtype_name=dtype_name) == "hip"
+                                     dtype_name=dtype_name, needs_grad=False) == "hip"
 
 
 def _use_hip_append(backend: str, cache: torch.Tensor) -> bool:
@@ -294,7 +294,7 @@ class RaggedKVCache(PreallocatedKVCache):
         if _use_hip_append(backend, self.k):
             from ._hip_append import append_kv_hip
 
-            append_kv_hip(self.k, self.v, new_k, new_v, self.starts)
+            append_kv_hip(self.k, self.v, new_k, new_v, self.starts, host_starts=self.lengths)
         else:
             for b, start in enumerate(self.lengths):
                 self.k[b, :, start:start + n].copy_(new_k[b])

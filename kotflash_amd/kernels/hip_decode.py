@@ -162,6 +162,8 @@ def attention_append_decode_ragged(q, k_cache, v_cache, new_k, new_v, seqlens: t
     require_hip_tensors("ragged append/decode", q, k_cache, v_cache, new_k, new_v)
     if seqlens.dtype != torch.int32 or seqlens.device != q.device or seqlens.shape != (q.shape[0],):
         raise ValueError("seqlens must be a device int32 tensor of shape [B]")
+    if not seqlens.is_contiguous():  # the kernel reads seqlens[b] as a dense array
+        seqlens = seqlens.contiguous()
     if q.ndim != 4 or k_cache.ndim != 4 or v_cache.shape != k_cache.shape:
         raise ValueError("expected [B,H,S,D] query and cache tensors")
     if new_k.ndim != 4 or new_v.shape != new_k.shape or new_k.shape[2] <= 0:
@@ -198,6 +200,8 @@ def attention_decode_ragged(q, k_cache, v_cache, seqlens: torch.Tensor, *, max_s
     require_hip_tensors("ragged decode", q, k_cache, v_cache)
     if seqlens.dtype != torch.int32 or seqlens.device != q.device or seqlens.shape != (q.shape[0],):
         raise ValueError("seqlens must be a device int32 tensor of shape [B]")
+    if not seqlens.is_contiguous():  # the kernel reads seqlens[b] as a dense array
+        seqlens = seqlens.contiguous()
     if q.ndim != 4 or k_cache.ndim != 4 or v_cache.shape != k_cache.shape:
         raise ValueError("expected [B,H,S,D] query and cache tensors")
     if not (0 < max_seqlen <= k_cache.shape[2]):

@@ -5,15 +5,13 @@ import torch
 
 # Tolerances against fp32 references. O/LSE: atol = rtol = 2e-3 for fp16 and
 # 1e-2 for bf16; fp16 gradients: atol 1e-2 (the build target's figures).
-# bf16 gradients: atol 3e-2 + rtol 1e-2. P and dS are rounded to the input
-# dtype before their products (as in the reference, triton_backward.py:85,
-# :183-184), and with bf16's 8-bit mantissa that alone moves dK/dV by up to
-# 3e-2 at these shapes: PyTorch's own bf16 SDPA backward on identical inputs
-# measured 2.6e-2 (Hq=8, Hkv=2, S=64/80) and 3.2e-2 (B=2, Hq=16, S=4096, where
-# |dV| reaches 9.8 and one bf16 half-ulp is 0.031) against the same fp32
-# reference. test_bf16_gradients_no_worse_than_torch checks that relation.
+# bf16 gradients: atol 1e-2 + rtol 1e-2, the target's 1e-2 in its relative
+# form: a bf16 output cannot meet an absolute-only 1e-2 where |dV| ~ 9 (one
+# bf16 half-ulp there is 0.031). At config 3 the HIP backward has no element
+# outside it, while PyTorch's own bf16 SDPA backward has 5 dV elements outside
+# (test_config3_bf16_gradients_at_stated_bar prints both).
 FWD_TOL = {torch.float16: dict(atol=2e-3, rtol=2e-3), torch.bfloat16: dict(atol=1e-2, rtol=1e-2)}
-BWD_TOL = {torch.float16: dict(atol=1e-2, rtol=0.0), torch.bfloat16: dict(atol=3e-2, rtol=1e-2)}
+BWD_TOL = {torch.float16: dict(atol=1e-2, rtol=0.0), torch.bfloat16: dict(atol=1e-2, rtol=1e-2)}
 
 
 def seeded(shape, seed, *, dtype, scale=1.0, device="cuda"):
@@ -58,3 +56,17 @@ def assert_close(actual, expected, *, atol, rtol, what=""):
             f"(atol={atol}, rtol={rtol}); max abs err {float(err.max()):.3e}; worst at flat "
             f"index {idx}: got {float(a.flatten()[idx]):.6f} want {float(e.flatten()[idx]):.6f}"
         )
+
+
+def error_stats(actual, expected, *, atol, rtol):
+    """Per-tensor error figures against ``expected``: max abs error, max
+    relative error over elements with |expected| >= 1e-2 (smaller ones make
+    the ratio meaningless), and the count outside atol + rtol |expected|."""
+    a = actual.detach().float()
+    e = expected.detach().float().to(a.device)
+    err = (a - e).abs()
+    big = e.abs() >= 1e-2
+    rel = (err[big] / e.abs()[big]).max() if bool(big.any()) else torch.zeros(())
+    return {"max_abs": float(err.max()), "max_rel": float(rel),
+            "outside": int((err > atol + rtol * e.abs()).sum()), "numel": a.numel(),
+            "max_ref": float(e.abs().max())}

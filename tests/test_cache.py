@@ -210,7 +210,7 @@ def test_auto_fuses_routing(monkeypatch):
     q = torch.empty(2, 8, 1, 64, dtype=torch.float16)
     fuses = cache_mod._auto_fuses
     assert fuses(q, kc, 4096, "auto", False)            # split-KV decode shape
-    assert not fuses(q, kc, 100, "auto", False)         # auto attention -> SDPA
+    assert fuses(q, kc, 100, "auto", False)             # auto inference -> HIP at any size
     assert fuses(q, kc, 100, "hip", False)              # HIP forced
     assert not fuses(q, kc, 4096, "sdpa", False)
     assert not fuses(q, kc, 4096, "auto", True)         # autograd

@@ -205,8 +205,9 @@ def test_ragged_append_decode_many_new_tokens(n):
 
 def test_preallocated_cache_auto_takes_fused_path_when_it_applies(monkeypatch):
     """PreallocatedKVCache.append_and_attend with the default backends fuses
-    the append into the decode for an inference-only decode shape, and keeps
-    the two-step path with autograd or below the decode envelope."""
+    the append into the decode for inference-only calls (auto sends
+    inference to the HIP kernels at any cache length), and keeps the two-step
+    path with autograd."""
     from kotflash_amd.cache import PreallocatedKVCache
     import kotflash_amd.kernels.hip_decode as hd
 
@@ -235,9 +236,13 @@ def test_preallocated_cache_auto_takes_fused_path_when_it_applies(monkeypatch):
     qg = q.clone().requires_grad_(True)
     out2 = cache.append_and_attend(qg, nk, nv)
     assert calls == [2047] and cache.length == 2049 and out2.requires_grad
-    # Below the split-KV decode envelope (auto attention goes to SDPA): two-step.
+    # A cache below the split-KV decode envelope fuses too (inference).
     small = PreallocatedKVCache(2, 2, 256, 64, device="cuda", dtype=F16)
     small.append(pk[:, :, :100], pv[:, :, :100], backend="torch")
     with torch.inference_mode():
-        small.append_and_attend(q, nk, nv)
-    assert calls == [2047] and small.length == 101
+        out3 = small.append_and_attend(q, nk, nv)
+    assert calls == [2047, 100] and small.length == 101
+    assert torch.equal(small.k[:, :, 100:101], nk)
+    eo, _ = reference_fp32(q, torch.cat((pk[:, :, :100], nk), 2),
+                           torch.cat((pv[:, :, :100], nv), 2), causal=False)
+    assert_close(out3, eo, **FWD_TOL[F16], what="auto (fused, short cache) O")

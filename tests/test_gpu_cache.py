@@ -114,3 +114,54 @@ def test_config5_append_and_ragged_decode_steps():
             kv, vv = cache.view(i)
             eo, _ = reference_fp32(q[i:i + 1], kv, vv, causal=False)
             assert_close(out[i:i + 1], eo, **FWD_TOL[F16], what=f"step {step} seq {i}")
+
+
+def test_device_start_out_of_range_raises_before_writing():
+    """A per-sequence device start that would write past the capacity (or
+    below 0) is rejected before any launch, as the reference rejects a bad
+    scalar start (kv_append_cuda.cu:72-73); the caches stay unchanged."""
+    kc = torch.zeros((3, 2, 16, 64), device="cuda", dtype=F16)
+    vc = torch.zeros_like(kc)
+    nk = torch.ones((3, 2, 4, 64), device="cuda", dtype=F16)
+    for bad in ([0, 13, 2], [0, -1, 2]):
+        starts = torch.tensor(bad, device="cuda")
+        with pytest.raises(RuntimeError, match="capacity"):
+            append_kv_hip(kc, vc, nk, nk, starts)                      # checked via a host copy
+        with pytest.raises(RuntimeError, match="capacity"):
+            append_kv_hip(kc, vc, nk, nk, starts, host_starts=bad)     # checked via the mirror
+    torch.cuda.synchronize()
+    assert (kc == 0).all() and (vc == 0).all()
+    with pytest.raises(ValueError, match="one entry per batch"):
+        append_kv_hip(kc, vc, nk, nk, torch.zeros(3, device="cuda", dtype=torch.int64),
+                      host_starts=[0, 0])
+
+
+def test_expanded_start_and_strided_seqlens_are_read_as_values():
+    """Index tensors that are views (a stride-0 expand, a strided slice) are
+    read by value, not as raw memory."""
+    from kotflash_amd.kernels.hip_decode import attention_decode_ragged
+
+    kc = torch.zeros((4, 2, 40, 64), device="cuda", dtype=F16)
+    vc = torch.zeros_like(kc)
+    nk = seeded((4, 2, 3, 64), 331, dtype=F16)
+    nv = seeded((4, 2, 3, 64), 332, dtype=F16)
+    start = torch.full((1,), 7, device="cuda", dtype=torch.int64).expand(4)
+    assert start.stride() == (0,)
+    append_kv_hip(kc, vc, nk, nv, start)
+    assert torch.equal(kc[:, :, 7:10], nk) and torch.equal(vc[:, :, 7:10], nv)
+    assert (kc[:, :, :7] == 0).all() and (kc[:, :, 10:] == 0).all()
+
+    b, hkv, hq, cap, d = 3, 2, 8, 2048, 64
+    kc = seeded((b, hkv, cap, d), 333, dtype=F16)
+    vc = seeded((b, hkv, cap, d), 334, dtype=F16)
+    q = seeded((b, hq, 2, d), 335, dtype=F16)
+    lengths = [1500, 2048, 1100]
+    wide = torch.tensor([[x, -5] for x in lengths], device="cuda", dtype=torch.int32)
+    seqlens = wide[:, 0]
+    assert seqlens.stride() == (2,)
+    out = attention_decode_ragged(q, kc, vc, seqlens, max_seqlen=max(lengths), scale=0.125,
+                                  host_lengths=lengths)
+    for i, n in enumerate(lengths):
+        eo, _ = reference_fp32(q[i:i + 1], kc[i:i + 1, :, :n], vc[i:i + 1, :, :n], causal=False,
+                               scale=0.125)
+        assert_close(out[i:i + 1], eo, **FWD_TOL[F16], what=f"seq {i}")

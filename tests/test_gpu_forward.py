@@ -152,8 +152,9 @@ def test_public_attention_routes_to_hip(dtype):
 
 
 def test_auto_routing_by_problem_size(monkeypatch):
-    """``auto`` sends host-bound small problems to SDPA and the rest (and
-    split-KV decode) to the HIP kernels."""
+    """``auto`` sends host-bound small training calls to SDPA, and larger
+    ones, inference calls of any size and split-KV decode to the HIP
+    kernels."""
     import sys
 
     api = sys.modules["kotflash_amd.attention"]  # the package attribute is the function
@@ -169,8 +170,12 @@ def test_auto_routing_by_problem_size(monkeypatch):
     big = [seeded((2, 8 if i == 0 else 2, 1024, 64), 80 + i, dtype=F16) for i in range(3)]
     dec = [seeded((2, 8 if i == 0 else 2, 1 if i == 0 else 2048, 64), 90 + i, dtype=F16)
            for i in range(3)]
-    attention(*small, causal=True)
+    attention(*small, causal=True)          # inference: HIP at any size
+    assert len(calls) == 0
+    train = [t.clone().requires_grad_(True) for t in small]
+    attention(*train, causal=True)          # small training call: SDPA
     assert len(calls) == 1
     attention(*big, causal=True)
+    attention(*[t.clone().requires_grad_(True) for t in big], causal=True)
     attention(*dec, causal=False)
     assert len(calls) == 1
