@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define KF_ABI_VERSION 3
+#define KF_ABI_VERSION 4
 
 enum kf_status {
   KF_OK = 0,
@@ -152,6 +152,28 @@ int kf_attn_decode(const void* q, const void* k, const void* v, void* o, float* 
                    const int64_t* v_strides, const int64_t* o_strides, float scale,
                    int num_splits, int dtype, void* workspace, size_t workspace_bytes,
                    void* stream);
+
+/*
+ * kf_attn_decode without a workspace argument: it allocates nothing and
+ * takes no caller memory beyond its inputs and outputs. No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The split partials go to a static device array of
+ * KF_DECODE_NOALLOC_SCRATCH_BYTES (32 MiB) that every GPU the library runs on
+ * holds until the process ends; a problem whose partials need more
+ * (kf_decode_workspace_bytes) is rejected with KF_EINVAL before any launch.
+ * Every call on a GPU shares that GPU's array: calls that overlap in time on
+ * one GPU (concurrent streams or threads) race. Same arguments, results and
+ * errors as kf_attn_decode otherwise (bit-identical outputs for the same
+ * num_splits).
+ */
+#define KF_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int kf_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o, float* lse,
+                           const int32_t* seqlens_k, int64_t B, int64_t Hq, int64_t Hkv,
+                           int64_t Sq, int64_t Sk, int64_t D, const int64_t* q_strides,
+                           const int64_t* k_strides, const int64_t* v_strides,
+                           const int64_t* o_strides, float scale, int num_splits, int dtype,
+                           void* stream);
 
 /*
  * K/V cache append: cache[b, h, start_b + t, :] = new[b, h, t, :] for K and V

@@ -19,7 +19,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libkotflash_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 KF_F16, KF_BF16 = 0, 1
 KF_BWD_DELTA, KF_BWD_DQ, KF_BWD_DKDV, KF_BWD_DKDV_FIXUP = 1, 2, 4, 8
 KF_BWD_ALL = KF_BWD_DELTA | KF_BWD_DQ | KF_BWD_DKDV | KF_BWD_DKDV_FIXUP
@@ -49,6 +49,8 @@ _SIGNATURES = {
     "kf_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I]),
     "kf_attn_decode": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                             _I64P, _I64P, _I64P, _I64P, _F, _I, _I, _P, _SZ, _P]),
+    "kf_attn_decode_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                                    _I64P, _I64P, _I64P, _I64P, _F, _I, _I, _P]),
     "kf_kv_append": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                           _I64P, _I64P, _I64P, _I64P, _I, _P]),
     "kf_attn_append_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
@@ -245,6 +247,28 @@ def decode(q, k, v, out, lse: Optional[torch.Tensor], seqlens: Optional[torch.Te
             _stream(q.device),
         )
     _check(rc, "kf_attn_decode")
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20  # KF_DECODE_NOALLOC_SCRATCH_BYTES
+
+
+def decode_noalloc(q, k, v, out, lse: Optional[torch.Tensor], seqlens: Optional[torch.Tensor], *,
+                   scale: float, num_splits: int) -> None:
+    """kf_attn_decode_noalloc: the split-KV decode with its partials in the
+    library's static per-device scratch instead of a workspace (no device
+    allocation anywhere in the call; calls overlapping on one GPU race)."""
+    b, hq, sq, d = q.shape
+    _, hkv, sk, _ = k.shape
+    keep = [_strides(t) for t in (q, k, v, out)]
+    with _DeviceGuard(q.device):
+        rc = lib().kf_attn_decode_noalloc(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            lse.data_ptr() if lse is not None else None,
+            seqlens.data_ptr() if seqlens is not None else None,
+            b, hq, hkv, sq, sk, d, *keep,
+            float(scale), int(num_splits), dtype_code(q.dtype), _stream(q.device),
+        )
+    _check(rc, "kf_attn_decode_noalloc")
 
 
 def kv_append(k_cache, v_cache, new_k, new_v, *, start: int = 0,

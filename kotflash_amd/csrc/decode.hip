@@ -33,6 +33,9 @@
 //    workgroup was measured slower: either agent-scope release fences or
 //    agent-scope stores plus a counter atomic per workgroup cost more than
 //    the second launch.)
+#include <atomic>
+#include <mutex>
+
 #include "kf_common.hpp"
 #include "kf_host.hpp"
 
@@ -615,13 +618,14 @@ extern "C" size_t kf_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, 
   return (slots * (size_t)D * sizeof(float) + 255) / 256 * 256 + (slots * sizeof(float) + 255) / 256 * 256;
 }
 
-extern "C" int kf_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse,
-                              const int32_t* seqlens_k, int64_t B, int64_t Hq, int64_t Hkv,
-                              int64_t Sq, int64_t Sk, int64_t D, const int64_t* q_strides,
-                              const int64_t* k_strides, const int64_t* v_strides,
-                              const int64_t* o_strides, float scale, int num_splits, int dtype,
-                              void* workspace, size_t workspace_bytes, void* stream) {
-  const char* what = "kf_attn_decode";
+// Argument checks and launch of kf_attn_decode and kf_attn_decode_noalloc
+// (`what` names the entry point in error messages).
+static int decode_entry(const char* what, const void* q, const void* k, const void* v, void* o,
+                        float* lse, const int32_t* seqlens_k, int64_t B, int64_t Hq, int64_t Hkv,
+                        int64_t Sq, int64_t Sk, int64_t D, const int64_t* q_strides,
+                        const int64_t* k_strides, const int64_t* v_strides,
+                        const int64_t* o_strides, float scale, int num_splits, int dtype,
+                        void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_attn_common(what, B, Hq, Hkv, Sq, Sk, D, dtype);
   if (rc) return rc;
   if ((rc = check_tensor(what, "q", q, q_strides)) || (rc = check_tensor(what, "k", k, k_strides)) ||
@@ -664,6 +668,87 @@ extern "C" int kf_attn_decode(const void* q, const void* k, const void* v, void*
   p.scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   return dtype == KF_F16 ? dispatch_decode<_Float16, false>(p, s) : dispatch_decode<__bf16, false>(p, s);
+}
+
+extern "C" int kf_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse,
+                              const int32_t* seqlens_k, int64_t B, int64_t Hq, int64_t Hkv,
+                              int64_t Sq, int64_t Sk, int64_t D, const int64_t* q_strides,
+                              const int64_t* k_strides, const int64_t* v_strides,
+                              const int64_t* o_strides, float scale, int num_splits, int dtype,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  return decode_entry("kf_attn_decode", q, k, v, o, lse, seqlens_k, B, Hq, Hkv, Sq, Sk, D,
+                      q_strides, k_strides, v_strides, o_strides, scale, num_splits, dtype,
+                      workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// kf_attn_decode_noalloc: kf_attn_decode for callers that cannot allocate
+// device memory (code under HIP graph capture, serving loops). Its split
+// partials go to `scratch`, a fixed device array that every GPU the library
+// runs on holds until the process ends. In host code the name `scratch` is
+// only a stand-in for the device symbol: its device address is resolved once
+// per device with hipGetSymbolAddress (with that device current) and kept in
+// g_scratch_ptr; the kernels only ever receive that address.
+//
+// The decode kernels write every partial slot they later read (a split with
+// no visible key writes O_s = 0, LSE_s = -inf), so nothing is cleared
+// between calls. All calls on one GPU share its array: calls that overlap in
+// time on one GPU (concurrent streams or threads) race on it.
+constexpr size_t kDecodeScratchBytes = KF_DECODE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kDecodeScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
+std::mutex g_scratch_mutex;
+}  // namespace
+
+// Device address of `scratch` on the current device (resolved on the first
+// call for that device).
+static int decode_scratch(const char* what, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(KF_ELAUNCH, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return set_error(KF_EUNSUPPORTED, "%s: device index %d beyond the %d supported", what, dev,
+                     kMaxScratchDevices);
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || ptr == nullptr)
+        return set_error(KF_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                         what, dev, hipGetErrorString(e));
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return KF_OK;
+}
+
+extern "C" int kf_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o,
+                                      float* lse, const int32_t* seqlens_k, int64_t B, int64_t Hq,
+                                      int64_t Hkv, int64_t Sq, int64_t Sk, int64_t D,
+                                      const int64_t* q_strides, const int64_t* k_strides,
+                                      const int64_t* v_strides, const int64_t* o_strides,
+                                      float scale, int num_splits, int dtype, void* stream) {
+  const char* what = "kf_attn_decode_noalloc";
+  if (num_splits < 1) return set_error(KF_EINVAL, "%s: num_splits must be >= 1", what);
+  const size_t need = kf_decode_workspace_bytes(B, Hq, Hkv, Sq, D, num_splits);
+  if (need > kDecodeScratchBytes)
+    return set_error(KF_EINVAL, "%s: this problem needs %zu bytes of split partials, more than "
+                     "the %zu-byte static scratch; use kf_attn_decode with a workspace", what,
+                     need, kDecodeScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = decode_scratch(what, &ws);
+    if (rc) return rc;
+  }
+  return decode_entry(what, q, k, v, o, lse, seqlens_k, B, Hq, Hkv, Sq, Sk, D, q_strides,
+                      k_strides, v_strides, o_strides, scale, num_splits, dtype, ws,
+                      kDecodeScratchBytes, stream);
 }
 
 extern "C" int kf_attn_append_decode(const void* q, void* k_cache, void* v_cache, const void* new_k,

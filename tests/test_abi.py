@@ -175,3 +175,18 @@ def test_append_decode_workspace_has_one_extra_split():
             > lib.kf_decode_workspace_bytes(8, 32, 8, 16, 64, ns))
     # Zero cache keys: one (empty) cache split plus the new tokens' split.
     assert lib.kf_decode_num_splits(1, 4, 1, 1, 0, 64) == 1
+
+
+def test_decode_noalloc_rejects_problems_beyond_its_scratch():
+    """kf_attn_decode_noalloc refuses a problem whose split partials exceed
+    its static scratch, before touching the device (no kernel launch)."""
+    lib = _hip.lib()
+    b, hq, hkv, sq, d, splits = 64, 64, 8, 16, 128, 64
+    need = lib.kf_decode_workspace_bytes(b, hq, hkv, sq, d, splits)
+    assert need > _hip.NOALLOC_SCRATCH_BYTES
+    s = _arr(1 << 20, 1 << 16, 128)
+    rc = lib.kf_attn_decode_noalloc(0x1000, 0x2000, 0x3000, 0x4000, None, None, b, hq, hkv, sq,
+                                    4096, d, s, s, s, s, 0.1, splits, 0, None)
+    assert rc == 1
+    assert "static scratch" in lib.kf_last_error().decode()
+    assert lib.kf_decode_workspace_bytes(2, 8, 2, 1, 64, 64) <= _hip.NOALLOC_SCRATCH_BYTES
