@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define KF_ABI_VERSION 4
+#define KF_ABI_VERSION 5
 
 enum kf_status {
   KF_OK = 0,
@@ -152,6 +152,26 @@ int kf_attn_decode(const void* q, const void* k, const void* v, void* o, float* 
                    const int64_t* v_strides, const int64_t* o_strides, float scale,
                    int num_splits, int dtype, void* workspace, size_t workspace_bytes,
                    void* stream);
+
+/*
+ * LSE-weighted merge of split-KV partials computed elsewhere, e.g. by the
+ * GPUs of a sequence-sharded decode or by a caller's own split kernel:
+ *   O[b,h,i,:] = sum_s w_s part_o[s,b,h,i,:],  w_s = exp(LSE_s - M) / sum_t exp(LSE_t - M),
+ *   LSE[b,h,i] = M + ln(sum_t exp(LSE_t - M)),  M = max_s LSE_s,
+ * with a row whose splits are all empty (LSE_s = -inf) giving O = 0 and
+ * LSE = -inf. part_o is fp32 contiguous [num_splits, B, H, S, D] (16-byte
+ * aligned), part_lse fp32 contiguous [num_splits, B, H, S] (natural log); o
+ * is [B, H, S, D] in `dtype` with a unit head_dim stride, strides in
+ * elements (multiples of 4, 8-byte aligned base); lse (nullable) fp32
+ * contiguous [B, H, S]. D is a multiple of 4 up to 128. One launch, one wave
+ * per output row. Replaces _attention_fwd_split_kv_reduce (reference
+ * kotflash/kernels/triton_forward.py:269-349), the merge the reference runs
+ * after its split kernel (:430-444); kf_attn_decode runs the same merge on
+ * its own partials.
+ */
+int kf_lse_merge(const float* part_o, const float* part_lse, void* o, float* lse,
+                 int64_t num_splits, int64_t B, int64_t H, int64_t S, int64_t D,
+                 const int64_t* o_strides, int dtype, void* stream);
 
 /*
  * kf_attn_decode without a workspace argument: it allocates nothing and

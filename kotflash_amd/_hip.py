@@ -19,7 +19,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libkotflash_amd.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 KF_F16, KF_BF16 = 0, 1
 KF_BWD_DELTA, KF_BWD_DQ, KF_BWD_DKDV, KF_BWD_DKDV_FIXUP = 1, 2, 4, 8
 KF_BWD_ALL = KF_BWD_DELTA | KF_BWD_DQ | KF_BWD_DKDV | KF_BWD_DKDV_FIXUP
@@ -49,6 +49,7 @@ _SIGNATURES = {
     "kf_decode_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I]),
     "kf_attn_decode": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                             _I64P, _I64P, _I64P, _I64P, _F, _I, _I, _P, _SZ, _P]),
+    "kf_lse_merge": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64P, _I, _P]),
     "kf_attn_decode_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                     _I64P, _I64P, _I64P, _I64P, _F, _I, _I, _P]),
     "kf_kv_append": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
@@ -247,6 +248,20 @@ def decode(q, k, v, out, lse: Optional[torch.Tensor], seqlens: Optional[torch.Te
             _stream(q.device),
         )
     _check(rc, "kf_attn_decode")
+
+
+def lse_merge(part_o, part_lse, out, lse: Optional[torch.Tensor]) -> None:
+    """kf_lse_merge: O (and LSE) from fp32 split partials part_o [S', B, H,
+    Sq, D] and part_lse [S', B, H, Sq]."""
+    ns, b, h, sq, d = part_o.shape
+    keep = _strides(out)
+    with _DeviceGuard(out.device):
+        rc = lib().kf_lse_merge(
+            part_o.data_ptr(), part_lse.data_ptr(), out.data_ptr(),
+            lse.data_ptr() if lse is not None else None, ns, b, h, sq, d, keep,
+            dtype_code(out.dtype), _stream(out.device),
+        )
+    _check(rc, "kf_lse_merge")
 
 
 NOALLOC_SCRATCH_BYTES = 32 << 20  # KF_DECODE_NOALLOC_SCRATCH_BYTES

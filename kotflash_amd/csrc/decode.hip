@@ -431,49 +431,39 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
 // a column then combine with lane swaps (v_permlane16/32_swap).
 constexpr int kMergeU = 16;
 
+// One output row: orr / lrr address split s's O row at s * ostride floats
+// and its LSE at s * lstride floats; every offset must fit 32 bits (checked
+// by the callers' hosts).
 template <typename T, int QL>
-__global__ __launch_bounds__(64) void merge_kernel(const DecParams p) {
+__device__ inline void merge_row(__amdgpu_buffer_rsrc_t orr, __amdgpu_buffer_rsrc_t lrr,
+                                 uint32_t ostride, uint32_t lstride, int nsplit, int D,
+                                 uint16_t* out_row, float* lse_out) {
   constexpr int SW = 64 / QL;
   const int lane = threadIdx.x;
-  const int RB = p.rb_rows;
-  const int R = p.G * p.Sq;
-  // blockIdx -> (b, kvh, packed row rho); partial rows are grouped by row block.
-  const int rho_all = blockIdx.x % R;
-  const int bk = blockIdx.x / R;
-  const int kvh = bk % p.Hkv, b = bk / p.Hkv;
-  const int rb = rho_all / RB, r = rho_all % RB;
-  const int grp = (b * p.Hkv + kvh) * p.nrb + rb;
-  const int g = rho_all / p.Sq, i = rho_all % p.Sq;
-  const int h = kvh * p.G + g;
-  // Row r of every split's partial: O at (s * RB + r) * D floats, LSE at s * RB + r.
-  const auto orr = make_rsrc(p.part_o + ((int64_t)grp * p.nsplit * RB + r) * p.D,
-                             (uint32_t)(((int64_t)(p.nsplit - 1) * RB * p.D + p.D) * 4));
-  const auto lrr = make_rsrc(p.part_lse + (int64_t)grp * p.nsplit * RB + r,
-                             (uint32_t)(((int64_t)(p.nsplit - 1) * RB + 1) * 4));
   const int q = lane % QL, sl = lane / QL;
-  const bool col = 4 * q < p.D;
+  const bool col = 4 * q < D;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float den = 0.f, mrun = kNegInf;  // running reference max of this lane's chunks (log2 units)
-  for (int c0 = 0; c0 < p.nsplit; c0 += kMergeU * SW) {
+  for (int c0 = 0; c0 < nsplit; c0 += kMergeU * SW) {
     u32x4 v[kMergeU];
     float w[kMergeU];
     uint32_t lw[kMergeU];
 #pragma unroll
     for (int u = 0; u < kMergeU; ++u) {
       const int s2 = c0 + sl + SW * u;
-      lw[u] = __builtin_amdgcn_raw_buffer_load_b32(lrr, s2 < p.nsplit ? (uint32_t)(s2 * RB) * 4u : kOOB, 0, 0);
+      lw[u] = __builtin_amdgcn_raw_buffer_load_b32(lrr, s2 < nsplit ? (uint32_t)s2 * lstride * 4u : kOOB, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < kMergeU; ++u) {
       const int s2 = c0 + sl + SW * u;
-      v[u] = buf_load16(orr, s2 < p.nsplit && col ? (uint32_t)(s2 * RB * p.D + 4 * q) * 4u : kOOB);
+      v[u] = buf_load16(orr, s2 < nsplit && col ? ((uint32_t)s2 * ostride + 4u * q) * 4u : kOOB);
     }
     // Keep every load of the chunk ahead of the first use: left alone, the
     // scheduler recycles early result registers and waits for them mid-batch.
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kMergeU; ++u)
-      w[u] = c0 + sl + SW * u < p.nsplit ? __uint_as_float(lw[u]) * kLog2e : kNegInf;
+      w[u] = c0 + sl + SW * u < nsplit ? __uint_as_float(lw[u]) * kLog2e : kNegInf;
     float mx = kNegInf;
 #pragma unroll
     for (int u = 0; u < kMergeU; ++u) mx = fmaxf(mx, w[u]);
@@ -508,10 +498,57 @@ __global__ __launch_bounds__(64) void merge_kernel(const DecParams p) {
     u32x2 wv;
     wv[0] = pack2<T>(acc[0] * inv, acc[1] * inv);
     wv[1] = pack2<T>(acc[2] * inv, acc[3] * inv);
-    *reinterpret_cast<u32x2*>(p.o + b * p.o_sb + h * p.o_sh + i * p.o_ss + 4 * q) = wv;
-    if (q == 0 && p.lse)
-      p.lse[((int64_t)b * p.Hq + h) * p.Sq + i] = dtot > 0.f ? (M + fast_log2(dtot)) * kLn2 : kNegInf;
+    *reinterpret_cast<u32x2*>(out_row + 4 * q) = wv;
+    if (q == 0 && lse_out) *lse_out = dtot > 0.f ? (M + fast_log2(dtot)) * kLn2 : kNegInf;
   }
+}
+
+template <typename T, int QL>
+__global__ __launch_bounds__(64) void merge_kernel(const DecParams p) {
+  const int RB = p.rb_rows;
+  const int R = p.G * p.Sq;
+  // blockIdx -> (b, kvh, packed row rho); partial rows are grouped by row block.
+  const int rho_all = blockIdx.x % R;
+  const int bk = blockIdx.x / R;
+  const int kvh = bk % p.Hkv, b = bk / p.Hkv;
+  const int rb = rho_all / RB, r = rho_all % RB;
+  const int grp = (b * p.Hkv + kvh) * p.nrb + rb;
+  const int g = rho_all / p.Sq, i = rho_all % p.Sq;
+  const int h = kvh * p.G + g;
+  // Row r of every split's partial: O at (s * RB + r) * D floats, LSE at s * RB + r.
+  const auto orr = make_rsrc(p.part_o + ((int64_t)grp * p.nsplit * RB + r) * p.D,
+                             (uint32_t)(((int64_t)(p.nsplit - 1) * RB * p.D + p.D) * 4));
+  const auto lrr = make_rsrc(p.part_lse + (int64_t)grp * p.nsplit * RB + r,
+                             (uint32_t)(((int64_t)(p.nsplit - 1) * RB + 1) * 4));
+  merge_row<T, QL>(orr, lrr, (uint32_t)(RB * p.D), (uint32_t)RB, p.nsplit, p.D,
+                   p.o + b * p.o_sb + h * p.o_sh + i * p.o_ss,
+                   p.lse ? p.lse + ((int64_t)b * p.Hq + h) * p.Sq + i : nullptr);
+}
+
+// Standalone merge of split partials in the reference's layout
+// (triton_forward.py:269-349): part_o [nsplit][B][H][S][D] and part_lse
+// [nsplit][B][H][S], fp32 and contiguous; one wave per output row.
+struct MergeParams {
+  const float* part_o;
+  const float* part_lse;
+  uint16_t* o;
+  float* lse;
+  int64_t o_sb, o_sh, o_ss;
+  int B, H, S, D, nsplit;
+};
+
+template <typename T, int QL>
+__global__ __launch_bounds__(64) void lse_merge_kernel(const MergeParams p) {
+  const int64_t rows = (int64_t)p.B * p.H * p.S;
+  const int64_t row = blockIdx.x;
+  const int i = (int)(row % p.S);
+  const int64_t bh = row / p.S;
+  const int h = (int)(bh % p.H), b = (int)(bh / p.H);
+  const auto orr = make_rsrc(p.part_o + row * p.D,
+                             (uint32_t)(((int64_t)(p.nsplit - 1) * rows * p.D + p.D) * 4));
+  const auto lrr = make_rsrc(p.part_lse + row, (uint32_t)(((int64_t)(p.nsplit - 1) * rows + 1) * 4));
+  merge_row<T, QL>(orr, lrr, (uint32_t)(rows * p.D), (uint32_t)rows, p.nsplit, p.D,
+                   p.o + b * p.o_sb + h * p.o_sh + i * p.o_ss, p.lse ? p.lse + row : nullptr);
 }
 
 // Packed rows per workgroup: 16-row MFMA blocks, up to four of them.
@@ -668,6 +705,45 @@ static int decode_entry(const char* what, const void* q, const void* k, const vo
   p.scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   return dtype == KF_F16 ? dispatch_decode<_Float16, false>(p, s) : dispatch_decode<__bf16, false>(p, s);
+}
+
+extern "C" int kf_lse_merge(const float* part_o, const float* part_lse, void* o, float* lse,
+                            int64_t num_splits, int64_t B, int64_t H, int64_t S, int64_t D,
+                            const int64_t* o_strides, int dtype, void* stream) {
+  const char* what = "kf_lse_merge";
+  if (part_o == nullptr || part_lse == nullptr)
+    return set_error(KF_EINVAL, "%s: part_o and part_lse must be non-null", what);
+  if (num_splits < 1 || B <= 0 || H <= 0 || S <= 0)
+    return set_error(KF_EINVAL, "%s: num_splits and all sizes must be positive", what);
+  if (D % 4 != 0 || D <= 0 || D > 128)
+    return set_error(KF_EUNSUPPORTED, "%s: head_dim must be a multiple of 4 in [4, 128], got %lld",
+                     what, (long long)D);
+  if (dtype != KF_F16 && dtype != KF_BF16)
+    return set_error(KF_EINVAL, "%s: dtype must be KF_F16 or KF_BF16", what);
+  if (o == nullptr || o_strides == nullptr) return set_error(KF_EINVAL, "%s: o is null", what);
+  if (!aligned8(o) || o_strides[0] % 4 || o_strides[1] % 4 || o_strides[2] % 4 ||
+      o_strides[0] < 0 || o_strides[1] < 0 || o_strides[2] < 0)
+    return set_error(KF_EINVAL, "%s: o must be 8-byte aligned with strides that are non-negative "
+                     "multiples of 4 elements", what);
+  if (!aligned16(part_o) || (reinterpret_cast<uintptr_t>(part_lse) & 3u) != 0)
+    return set_error(KF_EINVAL, "%s: part_o must be 16-byte and part_lse 4-byte aligned", what);
+  const int64_t rows = B * H * S;
+  if (rows > 0x7fffffff || num_splits * rows * D * 4 > 0x7fffffffLL)
+    return set_error(KF_EUNSUPPORTED, "%s: partials beyond 2 GiB", what);
+  MergeParams p{};
+  p.part_o = part_o; p.part_lse = part_lse; p.o = (uint16_t*)o; p.lse = lse;
+  p.o_sb = o_strides[0]; p.o_sh = o_strides[1]; p.o_ss = o_strides[2];
+  p.B = (int)B; p.H = (int)H; p.S = (int)S; p.D = (int)D; p.nsplit = (int)num_splits;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)rows);
+  if (dtype == KF_F16) {
+    if (D <= 64) hipLaunchKernelGGL((lse_merge_kernel<_Float16, 16>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((lse_merge_kernel<_Float16, 32>), grid, dim3(64), 0, s, p);
+  } else {
+    if (D <= 64) hipLaunchKernelGGL((lse_merge_kernel<__bf16, 16>), grid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL((lse_merge_kernel<__bf16, 32>), grid, dim3(64), 0, s, p);
+  }
+  return check_launch(what);
 }
 
 extern "C" int kf_attn_decode(const void* q, const void* k, const void* v, void* o, float* lse,

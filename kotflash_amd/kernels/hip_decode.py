@@ -220,3 +220,34 @@ def attention_decode_ragged(q, k_cache, v_cache, seqlens: torch.Tensor, *, max_s
     out, lse = _decode(q, k_view, v_view, seqlens, float(scale), with_lse=with_lse,
                        host_lengths=host_lengths)
     return (out, lse) if with_lse else out
+
+
+def lse_merge(part_o: torch.Tensor, part_lse: torch.Tensor, *, dtype: torch.dtype = torch.float16):
+    """Merge split-KV partials with their LSE weights (reference
+    triton_forward.py:269-349): part_o fp32 [splits, B, H, Sq, D] and part_lse
+    fp32 [splits, B, H, Sq] (natural log; -inf marks an empty split) give
+    O [B, H, Sq, D] in ``dtype`` and LSE [B, H, Sq] in fp32. One launch of
+    kf_lse_merge. The partials may come from anywhere: another GPU's share of
+    a sequence-sharded decode, or the reference's own split layout."""
+    if not (isinstance(part_o, torch.Tensor) and isinstance(part_lse, torch.Tensor)):
+        raise TypeError("part_o and part_lse must be tensors")
+    if part_o.ndim != 5 or part_lse.shape != part_o.shape[:4]:
+        raise ValueError("part_o must be [splits, B, H, Sq, D] and part_lse [splits, B, H, Sq]")
+    if part_o.dtype != torch.float32 or part_lse.dtype != torch.float32:
+        raise TypeError("split partials must be float32")
+    if not part_o.is_cuda or part_lse.device != part_o.device:
+        raise ValueError("split partials must be GPU tensors on one device")
+    if dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("the merged output dtype must be float16 or bfloat16")
+    d = part_o.shape[-1]
+    if d % 4 or not 4 <= d <= 128:
+        raise ValueError("head_dim must be a multiple of 4 in [4, 128]")
+    if not _hip.is_gfx950(part_o.device):
+        raise RuntimeError("lse_merge requires an AMD gfx950 (MI355X) device")
+    part_o = part_o.contiguous()
+    part_lse = part_lse.contiguous()
+    _, b, h, sq, _ = part_o.shape
+    out = torch.empty((b, h, sq, d), device=part_o.device, dtype=dtype)
+    lse = torch.empty((b, h, sq), device=part_o.device, dtype=torch.float32)
+    _hip.lse_merge(part_o, part_lse, out, lse)
+    return out, lse

@@ -190,3 +190,22 @@ def test_decode_noalloc_rejects_problems_beyond_its_scratch():
     assert rc == 1
     assert "static scratch" in lib.kf_last_error().decode()
     assert lib.kf_decode_workspace_bytes(2, 8, 2, 1, 64, 64) <= _hip.NOALLOC_SCRATCH_BYTES
+
+
+@pytest.mark.parametrize("kwargs,match", [
+    (dict(ns=0), "positive"),
+    (dict(D=130), "multiple of 4"),
+    (dict(D=6), "multiple of 4"),
+    (dict(dtype=3), "dtype"),
+    (dict(part_o=None), "non-null"),
+    (dict(part_o=0x1008), "aligned"),
+    (dict(o=0x3004), "aligned"),
+])
+def test_lse_merge_argument_validation(kwargs, match):
+    a = dict(part_o=0x1000, part_lse=0x2000, o=0x3000, ns=4, D=64, dtype=0)
+    a.update(kwargs)
+    s = _arr(2 * 8 * 64, 8 * 64, 64)
+    rc = _hip.lib().kf_lse_merge(a["part_o"], a["part_lse"], a["o"], None, a["ns"], 2, 2, 8,
+                                 a["D"], s, a["dtype"], None)
+    assert rc != 0
+    assert match in _hip.lib().kf_last_error().decode()

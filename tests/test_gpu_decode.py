@@ -191,3 +191,52 @@ def test_decode_merge_many_splits(d):
     eo, el = reference_fp32(q, k, v, causal=False)
     assert_close(out, eo, **FWD_TOL[F16], what="O")
     assert_close(lse, el, **FWD_TOL[F16], what="LSE")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("d", [64, 128, 72, 20])
+def test_lse_merge_matches_oracle(dtype, d):
+    """kf_lse_merge on partials in the reference's split layout
+    (triton_forward.py:269-349) against the oracle's merge: random partials
+    with empty splits (LSE = -inf) and one row whose splits are all empty."""
+    from kotflash_amd.kernels.hip_decode import lse_merge
+    from oracle import attention_oracle as orc
+
+    g = torch.Generator().manual_seed(940 + d)
+    ns, b, h, sq = 37, 2, 3, 5
+    part_o = torch.randn(ns, b, h, sq, d, generator=g)
+    part_lse = torch.randn(ns, b, h, sq, generator=g) * 4
+    part_lse[3] = float("-inf")                 # an empty split for every row
+    part_lse[:, 1, 2, 4] = float("-inf")        # a row with no visible key at all
+    part_o[:, 1, 2, 4] = 0.0
+    out, lse = lse_merge(part_o.cuda(), part_lse.cuda(), dtype=dtype)
+    eo, el = orc.split_kv_merge(part_o.numpy(), part_lse.numpy())
+    assert out.dtype == dtype and lse.shape == (b, h, sq)
+    assert_close(out, torch.from_numpy(eo), **FWD_TOL[dtype], what="merged O")
+    finite = torch.ones(b, h, sq, dtype=torch.bool)
+    finite[1, 2, 4] = False
+    assert_close(lse.cpu()[finite], torch.from_numpy(el)[finite], atol=1e-5, rtol=1e-5,
+                 what="merged LSE")
+    assert torch.isneginf(lse[1, 2, 4]) and (out[1, 2, 4] == 0).all()
+
+
+def test_lse_merge_of_oracle_split_partials_is_full_attention():
+    """Partials from the oracle's split kernel (uneven chunks, a ragged
+    sequence whose later splits are empty) merged on the GPU equal dense
+    attention: the merge is exact up to the output rounding."""
+    from kotflash_amd.kernels.hip_decode import lse_merge
+    from oracle import attention_oracle as orc
+
+    q = seeded((2, 8, 3, 64), 950, dtype=F16)
+    k = seeded((2, 2, 1500, 64), 951, dtype=F16)
+    v = seeded((2, 2, 1500, 64), 952, dtype=F16)
+    lengths = [1500, 700]
+    n = lambda t: t.cpu().float().numpy()
+    po, pl = orc.split_kv_partials(n(q), n(k), n(v), scale=0.125, num_splits=6, chunk_n=256,
+                                   seqlens=lengths)
+    out, lse = lse_merge(torch.from_numpy(po).float().cuda(), torch.from_numpy(pl).float().cuda())
+    for i, L in enumerate(lengths):
+        eo, el = reference_fp32(q[i:i + 1], k[i:i + 1, :, :L], v[i:i + 1, :, :L], causal=False,
+                                scale=0.125)
+        assert_close(out[i:i + 1], eo, **FWD_TOL[F16], what=f"O seq {i}")
+        assert_close(lse[i:i + 1], el, atol=1e-4, rtol=1e-5, what=f"LSE seq {i}")
