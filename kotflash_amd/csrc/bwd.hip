@@ -473,6 +473,14 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
         trb[db][hi] = s0 + (uint32_t)Tile::elem(r, col) * 2u;
         trb2[db][hi] = trb[db][hi] + 2u * kStageBytes;
       }
+    // The stage-2 bases are opaque to the optimizer: seeing them as base +
+    // 65536 it drops them and recomputes every stage-2 read address with a
+    // v_add_u32 (the offset exceeds the 16-bit ds_read immediate), 64 extra
+    // VALU instructions in every third unit.
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) asm volatile("" : "+v"(rdq2[ks]));
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) asm volatile("" : "+v"(trb2[db][0]), "+v"(trb2[db][1]));
   }
 
   const int64_t group_units = p.units / p.ngroups;
