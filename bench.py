@@ -23,6 +23,8 @@ One JSON line on stdout (everything else goes to stderr):
   fp16): microseconds per call (split-KV kernel + LSE merge) from HIP-graph
   replays of back-to-back calls over 32 rotating K/V sets (537 MB, larger than
   the 256 MB Infinity Cache), and HBM GB/s of the 16,781,376 algorithmic bytes.
+  ``decode.floor`` times probe kernels in the same setting: the decode's K/V
+  loads alone, those followed by a merge-shaped launch, and an empty launch.
 * ``configs``: the other BASELINE configurations timed on the GPU: config 1
   (forward only), config 2 over Sk in {2048, 4096, 8192, 16384}, config 3 in
   bf16, config 4 (non-causal MHA fwd+bwd, D = 72 and 96) and config 5 (64
@@ -268,6 +270,91 @@ def bench_decode(torch, _hip, dtype, sk, replays=20):
                 batch_tokens_per_s=b * sq / (us * 1e-6), algorithmic_bytes=nbytes,
                 hbm_gbps=nbytes / (us * 1e-6) / 1e9, hbm_frac=nbytes / (us * 1e-6) / PEAK_HBM,
                 timing="HIP graph replays of 32 back-to-back calls over 32 K/V sets (537 MB)")
+
+
+def bench_decode_floor(torch, _hip, sk=16384, replays=20):
+    """The decode's floor at config 2 (Sk=16384), in the setting of
+    bench_decode (HIP-graph replays of 32 back-to-back calls over 32 K/V
+    sets): the kernels of libkotflash_probe.so (kotflash_amd/csrc/probe)
+    issue exactly the decode's K/V loads and nothing else, a merge-shaped
+    second launch, or an empty launch; the decode itself runs beside them.
+    Returns microseconds per call, or None when the probe library is not
+    built."""
+    import ctypes
+    from pathlib import Path
+
+    path = Path(__file__).resolve().parent / "kotflash_amd" / "libkotflash_probe.so"
+    if not path.is_file():
+        return None
+    lib = ctypes.CDLL(str(path))
+    P, I, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    lib.kfp_stream.argtypes = [P, P, P, I64, I64, I64, I64, I, P]
+    lib.kfp_merge_like.argtypes = [P, P, I64, I, I64, P]
+    lib.kfp_empty.argtypes = [P]
+    for f in (lib.kfp_stream, lib.kfp_merge_like, lib.kfp_empty):
+        f.restype = I
+    c = dict(CFG2, Sk=sk)
+    b, hq, hkv, sq, d = c["B"], c["Hq"], c["Hkv"], c["Sq"], c["D"]
+    nsets = 32
+    ks = [seeded(torch, (b, hkv, sk, d), 1000 + i, torch.float16) for i in range(nsets)]
+    vs = [seeded(torch, (b, hkv, sk, d), 2000 + i, torch.float16) for i in range(nsets)]
+    q = seeded(torch, (b, hq, sq, d), 3000, torch.float16)
+    out = torch.empty_like(q)
+    splits = _hip.decode_num_splits(b, hq, hkv, sq, sk, d)
+    chunk = -(-sk // splits)
+    ws = torch.empty(max(256, _hip.decode_workspace_bytes(b, hq, hkv, sq, d, splits)),
+                     device=q.device, dtype=torch.uint8)
+    sink = torch.empty(b * hkv * splits * 4, device=q.device, dtype=torch.int32)
+    rows = b * hq * sq
+    part = torch.zeros(rows * splits * d, device=q.device, dtype=torch.float32)
+    merged = torch.empty(rows * d, device=q.device, dtype=torch.float32)
+
+    def stream(i, st):
+        rc = lib.kfp_stream(ks[i].data_ptr(), vs[i].data_ptr(), sink.data_ptr(), b * hkv, sk, d,
+                            chunk, splits, st)
+        if rc:
+            raise RuntimeError("kfp_stream failed")
+
+    def merge(st):
+        if lib.kfp_merge_like(part.data_ptr(), merged.data_ptr(), rows, splits, d, st):
+            raise RuntimeError("kfp_merge_like failed")
+
+    def decode(i, st):
+        _hip.decode(q, ks[i], vs[i], out, None, None, scale=1.0 / math.sqrt(d),
+                    num_splits=splits, workspace=ws)
+
+    variants = {
+        "empty_launch": lambda st: [lib.kfp_empty(st) for _ in range(nsets)],
+        "stream": lambda st: [stream(i, st) for i in range(nsets)],
+        "stream_then_merge": lambda st: [f(st) for i in range(nsets)
+                                         for f in (lambda s2, i=i: stream(i, s2), merge)],
+        "decode": lambda st: [decode(i, st) for i in range(nsets)],
+    }
+    res = {}
+    for name, calls in variants.items():
+        stream_ = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream_):
+            calls(stream_.cuda_stream)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=stream_):
+                calls(stream_.cuda_stream)
+        graph.replay()
+        torch.cuda.synchronize()
+        a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(replays):
+            graph.replay()
+        z.record()
+        torch.cuda.synchronize()
+        res[name] = a.elapsed_time(z) * 1e3 / (replays * nsets)
+    nbytes = 2 * b * hkv * sk * d * 2 + b * hq * sq * d * 2 * 2 + b * hq * sq * 4
+    res = {f"{k}_us": v for k, v in res.items()}
+    res["stream_hbm_frac"] = nbytes / (res["stream_us"] * 1e-6) / PEAK_HBM
+    res["note"] = ("probe kernels (kotflash_amd/csrc/probe/decode_floor.hip) in the decode line's "
+                   "graph setting: the decode's K/V loads alone, then followed by a merge-shaped "
+                   "launch, and an empty launch")
+    return res
 
 
 def bench_config5(torch, _hip, steps=64, seed=500):
@@ -552,6 +639,9 @@ def main() -> int:
     ap.add_argument("--pmc-sample", action="store_true",
                     help="run one config 3 step plus a calibration fill/copy for rocprofv3 "
                          "--pmc and exit (prints no bench line)")
+    ap.add_argument("--decode-floor", action="store_true",
+                    help="run only the config 2 decode floor probes beside the decode (graph "
+                         "replays) for a kernel trace and exit (prints no bench line)")
     ap.add_argument("--only-config5", action="store_true",
                     help="run only the config 5 append/decode loops (two-launch and fused) for "
                          "a kernel trace and exit (prints no bench line)")
@@ -583,6 +673,9 @@ def main() -> int:
     if args.only_config5:
         log(json.dumps(bench_config5(torch, _hip)))
         return 0
+    if args.decode_floor:
+        log(json.dumps(bench_decode_floor(torch, _hip)))
+        return 0
 
     ms, wall_ms, dkdv_live, per, work, step_flops, prewarm_steps = bench_train(
         torch, _hip, dtype, args.steps, args.warmup, prewarm_ms=args.prewarm_ms)
@@ -604,6 +697,7 @@ def main() -> int:
                 "timing": "HIP events around each dK/dV launch on its stream in the timed steps"}
     decode = None if args.no_decode else bench_decode(torch, _hip, torch.float16, CFG2["Sk"])
     if decode:
+        decode["floor"] = bench_decode_floor(torch, _hip)
         log(f"decode: {decode}")
     side = None if args.no_side else side_configs(torch, _hip, max(20, args.steps // 4))
     if side:
