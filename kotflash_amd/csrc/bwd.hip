@@ -167,12 +167,16 @@ __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
 // a two-stage LDS ring by direct-to-LDS loads (no register staging), stored
 // unpadded with the swizzle of SwizzledTile so that every LDS read of the
 // tile body is a per-lane base register plus an immediate offset.
-template <typename T, int DT, bool CAUSAL>
+// KS: 16-column k-steps of the contractions over head_dim (S, dP and the row
+// deltas): DT / 16, or 5 for head dims up to 80 in a 96-wide tile, whose
+// last 16 columns are zero padding.
+template <typename T, int DT, int KS, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
   constexpr int BM = 128;
   constexpr int BN = 64;
   constexpr int CPR = DT / 8;
-  constexpr int NKS = DT / 16;
+  constexpr int NKS = KS;
+  static_assert(KS * 16 <= DT && KS * 16 > DT - 32, "KS covers the tile's head_dim");
   constexpr int NDB = DT / 32;
   constexpr int TB = BN * DT * 2;       // bytes of one K (or V) tile
   constexpr int STAGE_B = 2 * TB;       // K | V
@@ -421,13 +425,14 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
 //   P  = exp2(scale log2e S - LSE log2e),  dS = P (dP - delta)
 //   dV^T += dO^T P,  dK^T += Q^T dS      (A = transposed LDS reads, B = P / dS
 //                                         straight from the S / dP registers)
-template <typename T, int DT, bool CAUSAL>
+template <typename T, int DT, int KS, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const DkdvSplit sp) {
   constexpr int CPR = DT / 8;
   constexpr int QT = kBMQ * DT;        // elements of one Q (or dO) tile
   constexpr int NQI = CPR / 4;         // 1 KB DMA instructions per wave per tile
   constexpr int NST = 3;               // LDS ring stages
-  constexpr int NKS = DT / 16;
+  constexpr int NKS = KS;              // k-steps of S and dP (as in dq_kernel)
+  static_assert(KS * 16 <= DT && KS * 16 > DT - 32, "KS covers the tile's head_dim");
   constexpr int NDB = DT / 32;
   using Tile = SwizzledTile<CPR>;
   static_assert(kBMQ * CPR == 4 * 64 * NQI, "tile chunks must split into whole DMA instructions");
@@ -990,7 +995,7 @@ static size_t partial_bytes(int nwg, int64_t D) {
   return (size_t)2 * nwg * 2 * kBNK * head_tile(D) * sizeof(float);
 }
 
-template <typename T, int DT>
+template <typename T, int DT, int KS>
 static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) {
   // dq_kernel computes the row deltas itself: the delta launch is only needed
   // when the dK/dV stage runs without it.
@@ -1004,9 +1009,9 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
     p.nqt = cdiv(p.Sq, 128);
     const int64_t gq = (int64_t)p.nqt * p.B * p.Hq;
     if (causal)
-      hipLaunchKernelGGL((dq_kernel<T, DT, true>), dim3((unsigned)gq), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((dq_kernel<T, DT, KS, true>), dim3((unsigned)gq), dim3(256), 0, stream, p);
     else
-      hipLaunchKernelGGL((dq_kernel<T, DT, false>), dim3((unsigned)gq), dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((dq_kernel<T, DT, KS, false>), dim3((unsigned)gq), dim3(256), 0, stream, p);
     int rc = check_launch("kf_attn_bwd(dq)");
     if (rc) return rc;
   }
@@ -1018,9 +1023,9 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
     DkdvSplit sp;
     dkdv_split(sp, p.ngroups, p.G, p.nqt, p.nkt, causal, p.nwg);
     if (causal)
-      hipLaunchKernelGGL((dkdv_kernel<T, DT, true>), dim3((unsigned)p.nwg), dim3(256), 0, stream, p, sp);
+      hipLaunchKernelGGL((dkdv_kernel<T, DT, KS, true>), dim3((unsigned)p.nwg), dim3(256), 0, stream, p, sp);
     else
-      hipLaunchKernelGGL((dkdv_kernel<T, DT, false>), dim3((unsigned)p.nwg), dim3(256), 0, stream, p, sp);
+      hipLaunchKernelGGL((dkdv_kernel<T, DT, KS, false>), dim3((unsigned)p.nwg), dim3(256), 0, stream, p, sp);
     int rc = check_launch("kf_attn_bwd(dkdv)");
     if (rc) return rc;
   }
@@ -1044,10 +1049,13 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
 template <typename T>
 static int dispatch_bwd(const BwdParams& p, bool causal, int stages, hipStream_t stream) {
   switch (head_tile(p.D)) {
-    case 32: return launch_bwd<T, 32>(p, causal, stages, stream);
-    case 64: return launch_bwd<T, 64>(p, causal, stages, stream);
-    case 96: return launch_bwd<T, 96>(p, causal, stages, stream);
-    default: return launch_bwd<T, 128>(p, causal, stages, stream);
+    case 32: return launch_bwd<T, 32, 2>(p, causal, stages, stream);
+    case 64: return launch_bwd<T, 64, 4>(p, causal, stages, stream);
+    case 96:
+      // Head dims 72 and 80 end 16 columns before the tile does.
+      return p.D <= 80 ? launch_bwd<T, 96, 5>(p, causal, stages, stream)
+                       : launch_bwd<T, 96, 6>(p, causal, stages, stream);
+    default: return launch_bwd<T, 128, 8>(p, causal, stages, stream);
   }
 }
 

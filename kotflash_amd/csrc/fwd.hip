@@ -74,12 +74,16 @@ __device__ inline void fwd_map_block(int bid, int nqt, int B, int Hq, int Hkv, i
   }
 }
 
-template <typename T, int DT, int QB, bool CAUSAL>
+// KS is the number of 16-column k-steps of the S = K Q^T contraction: DT / 16,
+// or fewer when the head dim ends earlier inside the tile (D <= 80 in a
+// 96-wide tile needs 5): the skipped columns are zero padding on both sides.
+template <typename T, int DT, int KS, int QB, bool CAUSAL>
 __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdParams p) {
   constexpr int BM = 4 * QB * 32;
   constexpr int BN = 64;
   constexpr int CPR = DT / 8;           // 16-byte chunks per row
-  constexpr int NKS = DT / 16;          // MFMA k-steps over head_dim
+  constexpr int NKS = KS;               // MFMA k-steps over head_dim
+  static_assert(KS * 16 <= DT && KS * 16 > DT - 32, "KS covers the tile's head_dim");
   constexpr int NDB = DT / 32;          // 32-wide head_dim blocks of O^T
   constexpr int TB = BN * DT * 2;       // bytes of one K (or V) tile
   constexpr int STAGE_B = 2 * TB;       // K | V
@@ -349,7 +353,7 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
   }
 }
 
-template <typename T, int DT, int QB>
+template <typename T, int DT, int KS, int QB>
 static int launch_fwd(const FwdParams& prm, bool causal, hipStream_t stream) {
   FwdParams p = prm;
   constexpr int BM = 4 * QB * 32;
@@ -357,9 +361,9 @@ static int launch_fwd(const FwdParams& prm, bool causal, hipStream_t stream) {
   const int64_t grid = (int64_t)p.nqt * p.B * p.Hq;
   if (grid > 0x7fffffff) return set_error(KF_EUNSUPPORTED, "kf_attn_fwd: grid too large");
   if (causal)
-    hipLaunchKernelGGL((fwd_kernel<T, DT, QB, true>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((fwd_kernel<T, DT, KS, QB, true>), dim3((unsigned)grid), dim3(256), 0, stream, p);
   else
-    hipLaunchKernelGGL((fwd_kernel<T, DT, QB, false>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((fwd_kernel<T, DT, KS, QB, false>), dim3((unsigned)grid), dim3(256), 0, stream, p);
   return check_launch("kf_attn_fwd");
 }
 
@@ -368,10 +372,13 @@ static int dispatch_fwd(const FwdParams& p, bool causal, hipStream_t stream) {
   // One 32-row block per wave at two waves per SIMD: while one wave runs its
   // softmax on the VALU the other keeps the MFMA pipe busy.
   switch (head_tile(p.D)) {
-    case 32: return launch_fwd<T, 32, 1>(p, causal, stream);
-    case 64: return launch_fwd<T, 64, 1>(p, causal, stream);
-    case 96: return launch_fwd<T, 96, 1>(p, causal, stream);
-    default: return launch_fwd<T, 128, 1>(p, causal, stream);
+    case 32: return launch_fwd<T, 32, 2, 1>(p, causal, stream);
+    case 64: return launch_fwd<T, 64, 4, 1>(p, causal, stream);
+    case 96:
+      // Head dims 72 and 80 end 16 columns before the tile does.
+      return p.D <= 80 ? launch_fwd<T, 96, 5, 1>(p, causal, stream)
+                       : launch_fwd<T, 96, 6, 1>(p, causal, stream);
+    default: return launch_fwd<T, 128, 8, 1>(p, causal, stream);
   }
 }
 
