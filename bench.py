@@ -206,8 +206,10 @@ def pmc_sample(torch, _hip, dtype):
                            "fill 512 MiB", "copy 512 MiB"], "copy_bytes": 2 * n}
 
 
-def bench_api(torch, kf, dtype, steps, warmup):
-    """Same step through the public API: attention(backend="hip") + autograd."""
+def bench_api(torch, kf, dtype, steps, warmup, prewarm_ms=PREWARM_MS):
+    """Same step through the public API: attention(backend="hip") + autograd,
+    wall time over `steps` steps after the same pre-warm as the kernel
+    figure (a short run measures allocator and clock warm-up instead)."""
     c = CFG3
     q = seeded(torch, (c["B"], c["Hq"], c["S"], c["D"]), 301, dtype, 0.5).requires_grad_(True)
     k = seeded(torch, (c["B"], c["Hkv"], c["S"], c["D"]), 302, dtype, 0.5).requires_grad_(True)
@@ -218,6 +220,7 @@ def bench_api(torch, kf, dtype, steps, warmup):
         out = kf.attention(q, k, v, causal=True, backend="hip")
         torch.autograd.grad(out, (q, k, v), do)
 
+    prewarm(torch, step, prewarm_ms)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -681,7 +684,7 @@ def main() -> int:
         torch, _hip, dtype, args.steps, args.warmup, prewarm_ms=args.prewarm_ms)
     log(f"train step: {ms:.4f} ms (GPU events), {wall_ms:.4f} ms (wall); dkdv live "
         f"{dkdv_live:.4f} ms; isolated per kernel {per}")
-    api_ms = bench_api(torch, kf, dtype, max(5, args.steps // 5), 2)
+    api_ms = bench_api(torch, kf, dtype, max(20, args.steps // 5), 5, args.prewarm_ms)
     log(f"public API step: {api_ms:.4f} ms")
     kernels = {}
     for n, t in per.items():
