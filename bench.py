@@ -541,6 +541,7 @@ def bench_sdpa_comparison(torch, steps=20, warmup=5):
     import kotflash_amd as kf
 
     def timed(fn):
+        prewarm(torch, fn, PREWARM_MS)
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
@@ -558,7 +559,8 @@ def bench_sdpa_comparison(torch, steps=20, warmup=5):
         ("config1_fwd_us", dict(B=2, Hq=8, Hkv=2, S=512, D=64), True, False, 1.0),
         ("config2_decode_sk16384_us", dict(B=2, Hq=8, Hkv=2, S=1, Sk=16384, D=64), False, False, 1.0),
     )
-    out = {"timing": "HIP events over back-to-back public-API calls (host overhead included)"}
+    out = {"timing": "HIP events over back-to-back public-API calls (host overhead included), "
+                     "each after a 200 ms pre-warm"}
     for name, c, causal, bwd, sc in cases:
         sk = c.get("Sk", c["S"])
         q = seeded(torch, (c["B"], c["Hq"], c["S"], c["D"]), 901, torch.float16, sc).requires_grad_(bwd)
