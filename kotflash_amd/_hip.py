@@ -122,12 +122,42 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 _I64x4 = ctypes.c_int64 * 4
+_STRIDE_ARRAYS: dict = {}
 
 
 def _strides(t: torch.Tensor):
     """The tensor's strides as a ctypes int64[4] (passed where the C ABI
-    takes ``const int64_t*``; ctypes hands over the array's address)."""
-    return _I64x4(*t.stride())
+    takes ``const int64_t*``; ctypes hands over the array's address). The
+    library only reads them during the call, so one array per distinct
+    stride tuple is kept and reused (decode calls repeat the same few)."""
+    st = t.stride()
+    arr = _STRIDE_ARRAYS.get(st)
+    if arr is None:
+        if len(_STRIDE_ARRAYS) > 4096:
+            _STRIDE_ARRAYS.clear()
+        arr = _STRIDE_ARRAYS[st] = _I64x4(*st)
+    return arr
+
+
+_WORKSPACES: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A byte buffer of at least ``nbytes`` for a launch on the current
+    stream of ``device``. Launches on one stream run in order, so the stream
+    reuses one buffer (grown when needed); another stream gets its own, as
+    torch's caching allocator would hand it. During graph capture the buffer
+    is a fresh allocation from the graph's pool, so no cached buffer is baked
+    into a graph."""
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(max(nbytes, 256), device=device, dtype=torch.uint8)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, _stream(device))
+    buf = _WORKSPACES.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 256), device=torch.device("cuda", index), dtype=torch.uint8)
+        _WORKSPACES[key] = buf
+    return buf
 
 
 def _check(rc: int, what: str) -> None:

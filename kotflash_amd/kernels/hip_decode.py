@@ -58,7 +58,7 @@ def _decode(q, k, v, seqlens: Optional[torch.Tensor], scale: float, with_lse: bo
     else:
         splits = _hip.decode_num_splits(b, hq, hkv, sq, sk, d)
     nbytes = _hip.decode_workspace_bytes(b, hq, hkv, sq, d, splits)
-    ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8) if nbytes else None
+    ws = _hip.workspace(q.device, nbytes) if nbytes else None
     _hip.decode(q, k, v, out, lse, seqlens, scale=scale, num_splits=splits, workspace=ws)
     return out, lse
 
@@ -143,7 +143,7 @@ def _append_decode(q, k_cache, v_cache, new_k, new_v, lengths: Optional[torch.Te
     else:
         splits = _hip.decode_num_splits(b, hq, hkv, sq, max_length, d)
     nbytes = _hip.decode_workspace_bytes(b, hq, hkv, sq, d, splits + 1)
-    ws = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
+    ws = _hip.workspace(q.device, nbytes)
     _hip.append_decode(q, k_cache, v_cache, new_k, new_v, out, lse, lengths,
                        past_length=past_length, max_length=max_length, scale=scale,
                        num_splits=splits, workspace=ws)
