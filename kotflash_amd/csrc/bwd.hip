@@ -565,20 +565,37 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
     constexpr uint32_t kStatBytes = 4u * kBMQ * 4u;
     // Units are walked in order (query head g, query tile qt descending):
     // workgroups that start a tile row together read the same Q/dO tiles at
-    // the same time. `Walk` advances one unit without divisions.
+    // the same time. `Walk` advances one unit without divisions, and carries
+    // the row pointers of head kvh G + g, stepped when g changes, so that a
+    // unit's DMA set-up needs no 64-bit products.
     struct Walk {
       int g, qt;
+      const uint16_t* qp;  // Q rows of the head
+      const uint16_t* dp;  // dO rows
+      const float* sp;     // statistics rows: LSE log2(e) (wave 0), -delta (wave 1)
     };
+    const int h0 = kvh * p.G;
+    const uint16_t* q_h0 = p.q + b * p.q_sb + (int64_t)h0 * p.q_sh;
+    const uint16_t* do_h0 = p.dout + b * p.do_sb + (int64_t)h0 * p.do_sh;
+    const float* st_h0 = (wave == 0 ? p.lse2 : p.delta) + ((int64_t)b * p.Hq + h0) * p.Sq;
+    const uint32_t q_ext = rows_extent(p.Sq, p.q_ss, p.D);
+    const uint32_t do_ext = rows_extent(p.Sq, p.do_ss, p.D);
     auto walk_init = [&](int it) {
       Walk w;
       w.g = it / nq;
       w.qt = qs + nq - 1 - (it - w.g * nq);
+      w.qp = q_h0 + (int64_t)w.g * p.q_sh;
+      w.dp = do_h0 + (int64_t)w.g * p.do_sh;
+      w.sp = st_h0 + (int64_t)w.g * p.Sq;
       return w;
     };
     auto walk_next = [&](Walk& w) {
       if (--w.qt < qs) {
         w.qt = qs + nq - 1;
         ++w.g;
+        w.qp += p.q_sh;
+        w.dp += p.do_sh;
+        w.sp += p.Sq;
       }
     };
     constexpr int NDMA = 2 * NQI + 1;  // DMA instructions per unit (the last: LSE or delta rows)
@@ -587,17 +604,15 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
       uint32_t qso, dso, sso;  // soffsets: the unit's first row
       uint32_t lq, ls;         // M0 of this wave's first Q block and of its statistics row
     };
-    // A unit past the segment's end gets empty resources: its loads then only
-    // deposit zeros into the (free) stage, which keeps the issue unconditional.
+    // A unit past the segment's end gets empty resources (no load reaches
+    // memory, whatever the base): its loads then only deposit zeros into the
+    // (free) stage, which keeps the issue unconditional.
     auto dma_setup = [&](const Walk& w, int st, bool real) {
       Dma d;
-      const int h = kvh * p.G + (real ? w.g : 0);
       const int q0 = real ? w.qt * kBMQ : 0;
-      d.qr = make_rsrc(p.q + b * p.q_sb + h * p.q_sh, real ? rows_extent(p.Sq, p.q_ss, p.D) : 0u);
-      d.dor = make_rsrc(p.dout + b * p.do_sb + h * p.do_sh,
-                        real ? rows_extent(p.Sq, p.do_ss, p.D) : 0u);
-      const int64_t rb = ((int64_t)b * p.Hq + h) * p.Sq;
-      d.sr = make_rsrc(wave == 0 ? p.lse2 + rb : p.delta + rb, real ? (uint32_t)p.Sq * 4u : 0u);
+      d.qr = make_rsrc(w.qp, real ? q_ext : 0u);
+      d.dor = make_rsrc(w.dp, real ? do_ext : 0u);
+      d.sr = make_rsrc(w.sp, real ? (uint32_t)p.Sq * 4u : 0u);
       d.qso = (uint32_t)(q0 * p.q_ss) * 2u;
       d.dso = (uint32_t)(q0 * p.do_ss) * 2u;
       d.sso = (uint32_t)q0 * 4u;
