@@ -411,6 +411,42 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
   }
 }
 
+// Softmax plan of a dK/dV unit. Its 32 softmax elements, k = 16 qb + r for
+// block qb and S/dP register r, each take three stages (exponent argument,
+// exp2, dS and packing) in three consecutive MFMA slots; stage a of element
+// k runs in slot a(k). The elements are spread evenly from the first slot
+// after block 0's S/dP MFMAs (slot NSD) to the last slot from which block
+// 1's high half still reaches its first dV/dK MFMA. A block's low (high)
+// half is packed at the third stage of its element 7 (15) and consumed from
+// slot 2 NSD + qb NVK (+ 2 NDB) on; block 1 cannot start before its S/dP
+// MFMAs end (slot 2 NSD). Where the even spread breaks one of these, each
+// block takes one phase: block 0 the S/dP slots of block 1, block 1 the
+// dV/dK slots of block 0.
+template <int NSD, int NVK, int NDB>
+struct DkdvSoftPlan {
+  static constexpr int kFirst = NSD;
+  static constexpr int kLast = 2 * NSD + NVK + 2 * NDB - 3;
+  static constexpr int even(int k) { return kFirst + k * (kLast - kFirst) / 31; }
+  static constexpr int phased(int k) {
+    return k < 16 ? NSD + k / ((16 + NSD - 1) / NSD) : 2 * NSD + (k - 16) / ((16 + NVK - 1) / NVK);
+  }
+  static constexpr bool even_ok() {
+    for (int qb = 0; qb < 2; ++qb) {
+      const int lo = 2 * NSD + qb * NVK, hi = lo + 2 * NDB;
+      if (even(16 * qb + 7) + 2 >= lo || even(16 * qb + 15) + 2 >= hi) return false;
+    }
+    return even(16) >= 2 * NSD;
+  }
+  static constexpr int a(int k) { return even_ok() ? even(k) : phased(k); }
+  // First element whose stage a runs at slot m or later (a is
+  // non-decreasing): the elements starting in slot m are [at(m), at(m + 1)).
+  static constexpr int at(int m) {
+    int k = 0;
+    while (k < 32 && a(k) < m) ++k;
+    return k;
+  }
+};
+
 // ---------------------------------------------------------------------------
 // 3. dK/dV, key-stationary, stream-K over (KV group, key tile, head, query
 // tile) units.
@@ -640,16 +676,21 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
     // With one wave per SIMD nothing else hides latency, so the unit is
     // software-pipelined by hand as one stream of MFMA slots, the order pinned
     // with scheduling fences:
-    //   slots [0, NSD)          S/dP MFMAs of qb 0
-    //   slots [NSD, 2 NSD)      S/dP MFMAs of qb 1      + softmax of qb 0
-    //   slots [2 NSD, +NVK)     dV/dK MFMAs of qb 0     + softmax of qb 1
+    //   slots [0, NSD)          S/dP MFMAs of qb 0      + the DMA of unit + 2
+    //   slots [NSD, 2 NSD)      S/dP MFMAs of qb 1
+    //   slots [2 NSD, +NVK)     dV/dK MFMAs of qb 0
     //   slots [.., +NVK)        dV/dK MFMAs of qb 1
-    // (NSD = NVK = 16 at head_dim 128; smaller tiles run several softmax
-    // elements per slot.)
-    // Each slot also issues the LDS read of the operand LA slots ahead (a
-    // short window keeps few operand registers live) and, spread over the
-    // middle slots, the DMA of unit + 2. The MFMAs run on the matrix core
-    // while the interleaved VALU, LDS and memory instructions issue.
+    // (NSD = NVK = 16 at head_dim 128), with the softmax of both blocks
+    // spread over slots NSD .. (DkdvSoftPlan). Each slot also issues the LDS
+    // read of the operand LA slots ahead (a short window keeps few operand
+    // registers live). The DMA goes into the stage that unit - 1 used, free
+    // since the barrier at the top of this unit; issued in the first slots,
+    // which carry no softmax, it also has the longest time to land. The
+    // MFMAs run on the matrix core while the interleaved VALU, LDS and memory
+    // instructions issue. (Per-wave timestamps showed the slots that carried
+    // the whole softmax of a block running 60-70% over their MFMA time and
+    // the last phase at the MFMA rate; spreading the softmax and moving the
+    // DMA to the first slots took 2.4% off the kernel at config 3.)
     auto unit = [&](auto stc, int qrow0, const Dma& nd) {
       constexpr int st = decltype(stc)::value;
       constexpr int NSD = 2 * NKS;  // S/dP MFMAs per block
@@ -768,37 +809,33 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
       init_block(0);
       static_for<0, LA>([&](auto mc) { read_op(decltype(mc)::value); });
       __builtin_amdgcn_sched_barrier(0);
-      // The softmax of block 0 runs in the S/dP slots of block 1 and that of
-      // block 1 in the dV/dK slots of block 0: each finishes before the first
-      // MFMA that consumes its P/dS. EPS* elements per slot fit 16 in a phase.
-      constexpr int EPS0 = (16 + NSD - 1) / NSD;
-      constexpr int EPS1 = (16 + NVK - 1) / NVK;
-      constexpr int DMA0 = NSD;                 // first slot carrying a DMA
-      constexpr int DMAS = (2 * NSD + NVK - DMA0) / NDMA;  // slot spacing
-      static_assert(DMAS >= 1, "every DMA instruction gets a slot");
+      // Softmax elements per DkdvSoftPlan; each finishes before the first
+      // MFMA that consumes its P/dS.
+      using Plan = DkdvSoftPlan<NSD, NVK, NDB>;
+      constexpr int DMA0 = 1;                                        // first slot carrying a DMA
+      constexpr int DMAS = (NSD - 1) / NDMA > 0 ? (NSD - 1) / NDMA : 1;  // slot spacing
+      static_assert(DMA0 + (NDMA - 1) * DMAS < NSLOT, "every DMA instruction gets a slot");
+      static_assert(Plan::a(31) + 2 < NSLOT, "the softmax ends inside the unit");
       static_for<0, NSLOT>([&](auto mc) {
         constexpr int m = decltype(mc)::value;
         mfma_slot(m);
         if constexpr (m + LA < NSLOT) read_op(m + LA);
         if constexpr (m == NSD - 3) init_block(1);
-        // Softmax stages of block qb whose window starts at slot S: slot m
-        // runs stage a of its own elements, stage b of the previous slot's
-        // and stage c of the one before.
-        auto soft_slot = [&](auto qbc, auto sc, auto epsc) {
-          constexpr int qb = decltype(qbc)::value, S = decltype(sc)::value;
-          constexpr int EPS = decltype(epsc)::value;
-          static_for<0, EPS>([&](auto ec) {
-            constexpr int e = decltype(ec)::value;
-            constexpr int ra = (m - S) * EPS + e, rb = (m - S - 1) * EPS + e, rc = (m - S - 2) * EPS + e;
-            if constexpr (m >= S + 2 && rc >= 0 && rc < 16) soft_c(qb, rc);
-            if constexpr (m >= S + 1 && rb >= 0 && rb < 16) soft_b(qb, rb);
-            if constexpr (m >= S && ra < 16) soft_a(qb, ra);
-          });
-        };
-        soft_slot(std::integral_constant<int, 0>{}, std::integral_constant<int, NSD>{},
-                  std::integral_constant<int, EPS0>{});
-        soft_slot(std::integral_constant<int, 1>{}, std::integral_constant<int, 2 * NSD>{},
-                  std::integral_constant<int, EPS1>{});
+        // Slot m runs stage c of the elements that started two slots ago,
+        // stage b of those of the previous slot and stage a of its own, each
+        // in element order (a block half is packed after its last element).
+        static_for<Plan::at(m - 2), Plan::at(m - 1)>([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          soft_c(k / 16, k % 16);
+        });
+        static_for<Plan::at(m - 1), Plan::at(m)>([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          soft_b(k / 16, k % 16);
+        });
+        static_for<Plan::at(m), Plan::at(m + 1)>([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          soft_a(k / 16, k % 16);
+        });
         if constexpr (m >= DMA0 && (m - DMA0) % DMAS == 0 && (m - DMA0) / DMAS < NDMA)
           dma_issue(nd, (m - DMA0) / DMAS);
         __builtin_amdgcn_sched_barrier(0);
