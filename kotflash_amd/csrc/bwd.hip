@@ -345,7 +345,11 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
           op[m] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
       };
-      f32x16 s = zero16(), dp = zero16();
+      // dP^T starts at -delta of the lane's row, so dS = P (dP - delta) is
+      // one multiply per element.
+      f32x16 s = zero16(), dp;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dp[r] = -dlt;
       static_for<0, LA>([&](auto mc) { read_op(decltype(mc)::value); });
       __builtin_amdgcn_sched_barrier(0);
       // Raised priority while this wave issues MFMAs, so that the other wave
@@ -373,7 +377,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
         }
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp[r] = fast_exp2(s[r]) * (dp[r] - dlt);
+      for (int r = 0; r < 16; ++r) dp[r] = fast_exp2(s[r]) * dp[r];
       const u32x4 ds0 = pack8<T>(dp, 0), ds1 = pack8<T>(dp, 8);
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(1);
