@@ -157,3 +157,41 @@ def test_fused_append_decode_graph_replays():
         torch.cuda.synchronize()
         assert torch.equal(got, out) and torch.equal(got_lse, lse), f"replay {r}"
         assert bool(torch.isfinite(out).all())
+
+
+def test_decode_workspaces_per_stream_and_fresh_under_capture():
+    """The eager decode reuses one workspace per (device, stream): calls on
+    two streams at once must not share it, and a graph captured on one
+    stream must hold its own workspace, so replaying it on another stream
+    while eager calls run on the capturing stream races with nothing."""
+    q1 = seeded((2, 8, 1, 64), 1701, dtype=F16)
+    k1 = seeded((2, 2, 8192, 64), 1702, dtype=F16)
+    v1 = seeded((2, 2, 8192, 64), 1703, dtype=F16)
+    q2 = seeded((2, 8, 1, 64), 1711, dtype=F16)
+    k2 = seeded((2, 2, 8192, 64), 1712, dtype=F16)
+    v2 = seeded((2, 2, 8192, 64), 1713, dtype=F16)
+    ref1 = kf.attention(q1, k1, v1, causal=False, backend="hip")
+    ref2 = kf.attention(q2, k2, v2, causal=False, backend="hip")
+    assert not torch.equal(ref1, ref2)
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    for r in range(3):
+        with torch.cuda.stream(sa):
+            oa = kf.attention(q1, k1, v1, causal=False, backend="hip")
+        with torch.cuda.stream(sb):
+            ob = kf.attention(q2, k2, v2, causal=False, backend="hip")
+        torch.cuda.synchronize()
+        assert torch.equal(oa, ref1) and torch.equal(ob, ref2), f"two streams, round {r}"
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(sa):
+        with torch.cuda.graph(graph, stream=sa):
+            gout = kf.attention(q1, k1, v1, causal=False, backend="hip")
+    torch.cuda.synchronize()
+    for r in range(3):
+        with torch.cuda.stream(sb):
+            graph.replay()
+        with torch.cuda.stream(sa):
+            eager = kf.attention(q2, k2, v2, causal=False, backend="hip")
+        torch.cuda.synchronize()
+        assert torch.equal(gout, ref1), f"replay {r}"
+        assert torch.equal(eager, ref2), f"eager beside replay {r}"
