@@ -29,6 +29,7 @@
 //      number of fp32 partial copies plus a reduction pass (:198-332).
 // P and dS are rounded to the input dtype before the products that consume
 // them, as in the reference (:85, :183-184).
+#include <algorithm>
 #include <cstring>
 
 #include "kf_common.hpp"
@@ -923,9 +924,17 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
 // ---------------------------------------------------------------------------
 // 4. Fixup: kFixSub workgroups per key tile, kFixKeys keys each. Sums the partials
 // of tiles shared by several dkdv workgroups, zero-fills tiles that no query
-// can see, and leaves tiles one workgroup finished alone untouched.
+// can see, and leaves tiles one workgroup finished alone untouched. The host
+// skips the launch when no share boundary cuts a tile row and every tile is
+// seen (non-causal shapes whose shares end on tile rows, such as config 4):
+// its thousands of workgroups would all return at once, which still costs
+// about 15 us of dispatch.
 constexpr int kFixKeys = 16;  // keys per fixup workgroup
 constexpr int kFixSub = kBNK / kFixKeys;
+__host__ inline int dkdv_first_unseen_tile(int nqt, int nkt, bool causal) {
+  // dkdv_nq(kt) = nqt - 2 kt under the causal mask: zero from ceil(nqt / 2).
+  return causal ? std::min((nqt + 1) / 2, nkt) : nkt;
+}
 template <typename T, int DT, bool CAUSAL>
 __global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p, const DkdvSplit sp) {
   const int t = blockIdx.x / kFixSub, sub = blockIdx.x % kFixSub;
@@ -1005,12 +1014,14 @@ static size_t delta_bytes(int64_t B, int64_t Hq, int64_t Sq) {
 // came out at 2.5 units from per-workgroup timestamps, and a sweep of the
 // weight put the shortest launch at 4.5 to 6 units.
 constexpr int kSegmentCost8 = 40;
-static void dkdv_split(DkdvSplit& sp, int ngroups, int G, int nqt, int nkt, bool causal, int nwg) {
+// Returns the number of tile rows that a share boundary cuts (shared tiles).
+static int dkdv_split(DkdvSplit& sp, int ngroups, int G, int nqt, int nkt, bool causal, int nwg) {
   struct Key {
     int ngroups, G, nqt, nkt, causal, nwg;
   };
   thread_local Key last{-1, 0, 0, 0, 0, 0};
   thread_local DkdvSplit cached;
+  thread_local int cached_shared = 0;
   const Key k{ngroups, G, nqt, nkt, causal ? 1 : 0, nwg};
   if (memcmp(&k, &last, sizeof k) != 0) {
     int64_t total = 0, all_units = 0;
@@ -1019,7 +1030,7 @@ static void dkdv_split(DkdvSplit& sp, int ngroups, int G, int nqt, int nkt, bool
       if (units) total += (int64_t)ngroups * (8 * units + kSegmentCost8);
       all_units += (int64_t)ngroups * units;
     }
-    int w = 1;
+    int w = 1, shared = 0;
     int64_t base = 0, cost = 0;
     cached.start[0] = 0;
     // Tile rows in unit order: KV group outer, key tile inner.
@@ -1029,22 +1040,27 @@ static void dkdv_split(DkdvSplit& sp, int ngroups, int G, int nqt, int nkt, bool
         if (!units) continue;
         const int64_t row_cost = 8 * units + kSegmentCost8;
         // Boundaries whose target cost falls inside this tile row.
+        bool cut = false;
         while (w < nwg) {
           const int64_t target = (total * w + nwg - 1) / nwg;
           if (target > cost + row_cost) break;
           int64_t into = (target - cost - kSegmentCost8 + 7) / 8;
           into = into < 0 ? 0 : (into > units ? units : into);
           cached.start[w++] = (int)(base + into);
+          cut = cut || (into > 0 && into < units);
         }
+        shared += cut ? 1 : 0;
         cost += row_cost;
         base += units;
       }
     }
     while (w < nwg) cached.start[w++] = (int)all_units;
     cached.start[nwg] = (int)all_units;
+    cached_shared = shared;
     last = k;
   }
   sp = cached;
+  return cached_shared;
 }
 
 static size_t partial_bytes(int nwg, int64_t D) {
@@ -1089,15 +1105,19 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
     p.nqt = cdiv(p.Sq, kBMQ);
     p.nkt = cdiv(p.Sk, kBNK);
     p.units = dkdv_total_units(p.ngroups, p.G, p.nqt, p.nkt, causal);
-    const int64_t tiles = (int64_t)p.nkt * p.ngroups * kFixSub;
     DkdvSplit sp;
-    dkdv_split(sp, p.ngroups, p.G, p.nqt, p.nkt, causal, p.nwg);
-    if (causal)
-      hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, true>), dim3((unsigned)tiles), dim3(256), 0, stream, p, sp);
-    else
-      hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, false>), dim3((unsigned)tiles), dim3(256), 0, stream, p, sp);
-    int rc = check_launch("kf_attn_bwd(dkdv fixup)");
-    if (rc) return rc;
+    const int shared = dkdv_split(sp, p.ngroups, p.G, p.nqt, p.nkt, causal, p.nwg);
+    const int64_t unseen = (int64_t)p.ngroups * (p.nkt - dkdv_first_unseen_tile(p.nqt, p.nkt, causal));
+    if (shared > 0 || unseen > 0) {
+      const int64_t grid = (int64_t)p.nkt * p.ngroups * kFixSub;
+      if (grid > 0x7fffffff) return set_error(KF_EINVAL, "kf_attn_bwd: problem too large for one fixup launch");
+      if (causal)
+        hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, true>), dim3((unsigned)grid), dim3(256), 0, stream, p, sp);
+      else
+        hipLaunchKernelGGL((dkdv_fixup_kernel<T, DT, false>), dim3((unsigned)grid), dim3(256), 0, stream, p, sp);
+      int rc = check_launch("kf_attn_bwd(dkdv fixup)");
+      if (rc) return rc;
+    }
   }
   return KF_OK;
 }
