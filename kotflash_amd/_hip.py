@@ -265,19 +265,20 @@ def decode(q, k, v, out, lse: Optional[torch.Tensor], seqlens: Optional[torch.Te
            scale: float, num_splits: int, workspace: Optional[torch.Tensor]) -> None:
     b, hq, sq, d = q.shape
     _, hkv, sk, _ = k.shape
-    keep = [_strides(t) for t in (q, k, v, out)]
     ws_ptr = workspace.data_ptr() if workspace is not None else None
-    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    with _DeviceGuard(q.device):
+    ws_bytes = workspace.nbytes if workspace is not None else 0
+    dev = q.device
+    with _DeviceGuard(dev):
         rc = lib().kf_attn_decode(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
             lse.data_ptr() if lse is not None else None,
             seqlens.data_ptr() if seqlens is not None else None,
-            b, hq, hkv, sq, sk, d, *keep,
+            b, hq, hkv, sq, sk, d, _strides(q), _strides(k), _strides(v), _strides(out),
             float(scale), int(num_splits), dtype_code(q.dtype), ws_ptr, ws_bytes,
-            _stream(q.device),
+            _stream(dev),
         )
-    _check(rc, "kf_attn_decode")
+    if rc:
+        _check(rc, "kf_attn_decode")
 
 
 def lse_merge(part_o, part_lse, out, lse: Optional[torch.Tensor]) -> None:

@@ -20,7 +20,11 @@ import torch.nn.functional as F
 from . import _hip
 from ._planning import gfx950_profile_for_shapes, t4_profile_for_shapes
 from .kernels.hip_backward import attention_backward
-from .kernels.hip_decode import decode_supported_unchecked, strided_decode_supported
+from .kernels.hip_decode import (  # noqa: F401  strided_decode_supported: the reference's module name
+    decode_supported_unchecked,
+    strided_decode_supported,
+    validated_decode_supported,
+)
 from .kernels.hip_forward import attention_forward, triton_turing_supported
 
 BACKENDS = ("auto", "hip", "triton", "sdpa")
@@ -30,29 +34,33 @@ _DTYPE_NAMES = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.floa
 def _validate(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
     """Input contract of the reference (kotflash/attention.py:21-45), in the
     same order and with the same messages."""
-    if not all(isinstance(x, torch.Tensor) for x in (q, k, v)):
+    if not (isinstance(q, torch.Tensor) and isinstance(k, torch.Tensor)
+            and isinstance(v, torch.Tensor)):
         raise TypeError("q, k and v must be torch.Tensor instances")
-    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+    qs, ks, vs = q.shape, k.shape, v.shape
+    if len(qs) != 4 or len(ks) != 4 or len(vs) != 4:
         raise ValueError("Expected q/k/v in [batch, heads, sequence, head_dim] layout")
-    if q.shape[0] == 0:
+    if qs[0] == 0:
         raise ValueError("Batch dimension must be non-zero")
-    if q.shape[1] == 0 or k.shape[1] == 0:
+    if qs[1] == 0 or ks[1] == 0:
         raise ValueError("Head dimensions must be non-zero")
-    if q.shape[-1] == 0:
+    if qs[3] == 0:
         raise ValueError("Head dimension must be non-zero")
-    if q.shape[0] != k.shape[0] or q.shape[0] != v.shape[0]:
+    if qs[0] != ks[0] or qs[0] != vs[0]:
         raise ValueError("Batch dimensions must match")
-    if k.shape != v.shape:
+    if ks != vs:
         raise ValueError("K and V shapes must match")
-    if q.shape[-1] != k.shape[-1]:
+    if qs[3] != ks[3]:
         raise ValueError("Q/K/V head dimensions must match")
-    if q.shape[1] % k.shape[1] != 0:
+    if qs[1] % ks[1] != 0:
         raise ValueError("num_query_heads must be divisible by num_kv_heads (GQA/MQA)")
-    if q.device != k.device or q.device != v.device:
+    dev = q.device
+    if dev != k.device or dev != v.device:
         raise ValueError("Q/K/V must be on the same device")
-    if q.dtype != k.dtype or q.dtype != v.dtype:
+    dt = q.dtype
+    if dt != k.dtype or dt != v.dtype:
         raise ValueError("Q/K/V dtypes must match")
-    if q.shape[2] == 0 or k.shape[2] == 0:
+    if qs[2] == 0 or ks[2] == 0:
         raise ValueError("Sequence dimensions must be non-zero")
 
 
@@ -274,7 +282,7 @@ def attention(
 
     # Inference on preallocated caches: read the (padded) K/V views in place.
     if (explicit or route == "hip") and not causal and not needs_grad \
-            and strided_decode_supported(q, k, v):
+            and validated_decode_supported(q, k, v):
         return decode_supported_unchecked(q, k, v, float(scale))
 
     if explicit:

@@ -47,6 +47,27 @@ def strided_decode_supported(q, k, v) -> bool:
     return _hip.is_gfx950(q.device) and _hip.library_available()
 
 
+_DECODE_DTYPES = (torch.float16, torch.bfloat16)
+
+
+def validated_decode_supported(q, k, v) -> bool:
+    """``strided_decode_supported`` for inputs that already passed the public
+    ``attention``'s validation (tensors, 4-D, matching batch and head_dim,
+    head grouping, one device, one dtype): only the decode envelope, the
+    layouts and the device remain to check."""
+    if not q.is_cuda or q.dtype not in _DECODE_DTYPES:
+        return False
+    qs, ks = q.shape, k.shape
+    if qs[2] > GFX950_DECODE_MAX_SQ or ks[2] < GFX950_DECODE_MIN_SK:
+        return False
+    d = qs[3]
+    if d % 8 or not gfx950_head_dim_ok(d):
+        return False
+    if not (_hip.layout_ok(q) and _hip.layout_ok(k) and _hip.layout_ok(v)):
+        return False
+    return _hip.is_gfx950(q.device) and _hip.library_available()
+
+
 def _decode(q, k, v, seqlens: Optional[torch.Tensor], scale: float, with_lse: bool,
             host_lengths: Optional[Sequence[int]] = None):
     b, hq, sq, d = q.shape
@@ -76,8 +97,8 @@ def attention_forward_strided_decode(q, k, v, *, scale: float):
 
 def decode_supported_unchecked(q, k, v, scale: float):
     """``attention_forward_strided_decode`` for a caller that has just
-    checked ``strided_decode_supported(q, k, v)`` (the public ``attention``),
-    without checking again."""
+    checked ``validated_decode_supported(q, k, v)`` (the public
+    ``attention``), without checking again."""
     return _decode(q, k, v, None, float(scale), with_lse=False)[0]
 
 

@@ -240,3 +240,30 @@ def test_lse_merge_of_oracle_split_partials_is_full_attention():
                                 scale=0.125)
         assert_close(out[i:i + 1], eo, **FWD_TOL[F16], what=f"O seq {i}")
         assert_close(lse[i:i + 1], el, atol=1e-4, rtol=1e-5, what=f"LSE seq {i}")
+
+
+def test_validated_decode_check_agrees_with_the_full_one():
+    """The public ``attention``'s decode lane checks only what its validation
+    left open; on validated inputs it must decide as ``strided_decode_supported``."""
+    from kotflash_amd.kernels.hip_decode import strided_decode_supported, validated_decode_supported
+
+    cases = []
+    for dtype in (torch.float16, torch.bfloat16, torch.float32):
+        for sq, sk, d in ((1, 4096, 64), (16, 1024, 128), (17, 4096, 64), (1, 1023, 64),
+                          (1, 2048, 72), (1, 2048, 20), (4, 2048, 136)):
+            q = torch.zeros((2, 8, sq, d), device="cuda", dtype=dtype)
+            k = torch.zeros((2, 2, sk, d), device="cuda", dtype=dtype)
+            cases.append((q, k, k.clone()))
+    base = torch.zeros((2, 2, 4096 + 64, 64), device="cuda", dtype=torch.float16)
+    cases.append((torch.zeros((2, 8, 1, 64), device="cuda", dtype=torch.float16),
+                  base[:, :, :3000], base[:, :, :3000]))              # padded cache view
+    wide = torch.zeros((2, 2, 2048, 72), device="cuda", dtype=torch.float16)[..., :64]
+    cases.append((torch.zeros((2, 8, 1, 64), device="cuda", dtype=torch.float16), wide, wide))
+    odd = torch.zeros((2 * 2 * 2048 * 64 + 4,), device="cuda", dtype=torch.float16)[4:].view(2, 2, 2048, 64)
+    cases.append((torch.zeros((2, 8, 1, 64), device="cuda", dtype=torch.float16), odd, odd))
+    seen = set()
+    for q, k, v in cases:
+        full, lean = strided_decode_supported(q, k, v), validated_decode_supported(q, k, v)
+        assert full == lean, (tuple(q.shape), tuple(k.shape), k.stride(), q.dtype)
+        seen.add(full)
+    assert seen == {True, False}
