@@ -210,7 +210,11 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
       // issued one slot ahead and every MFMA waits for its operand.
       constexpr int NS = 2 * NKS;   // S slots
       constexpr int NPV = 4 * NDB;  // PV slots (db = j / 4, key step st = j % 4)
-      constexpr int LA = 4;
+      // Operand read-ahead in slots. For the 128-wide tile (16 S slots) 8 is
+      // the measured optimum at config 3 (A/B in one process, fp16 -3.2%,
+      // bf16 -3.4% against 4; 5, 6, 10 and 12 are slower and 16 spills);
+      // the narrower tiles are fastest at 4 (6 cost 1-7% there).
+      constexpr int LA = DT == 128 ? 8 : 4;
       u32x4 kop[NS], vop[NPV];
       auto read_k = [&](int m) {
         const uint32_t off = ST * STAGE_B + (m / NKS) * 32 * CPR * 16;
