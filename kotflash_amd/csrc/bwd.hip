@@ -332,7 +332,14 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
       // every MFMA waits for its operand.
       constexpr int NSD = 2 * NKS;
       constexpr int NDQ = 2 * NDB;
-      constexpr int LA = 4;
+      // Operand read-ahead in slots: 5 for the 128-wide tile, the measured
+      // optimum at config 3 (A/B in one process, fp16 -3.9%, bf16 -4.1%
+      // against 4; 3 is level, 6 slower by 5%, 8 by 17%). At 5 the register
+      // allocator spills 12 bytes to scratch (vector scratch_store/load): the
+      // one reload inside the tile loop restores a DMA offset right after the
+      // tile-end vmcnt(0) and barrier, so it drains nothing that was not
+      // drained already. Narrower tiles stay at 4.
+      constexpr int LA = DT == 128 ? 5 : 4;
       u32x4 op[NSD + NDQ];
       auto read_op = [&](int m) {
         if (m < NSD) {
