@@ -267,3 +267,25 @@ def test_validated_decode_check_agrees_with_the_full_one():
         assert full == lean, (tuple(q.shape), tuple(k.shape), k.stride(), q.dtype)
         seen.add(full)
     assert seen == {True, False}
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16])
+def test_long_context_decode(dtype):
+    """A 256K-key cache (D=128, MQA with 16 query heads, 4 new tokens per
+    sequence): the split plan's largest chunks, per-head K/V slices of
+    64 MiB and the merge of many splits, against dense fp32 attention, and
+    the public API on a padded view of a longer cache."""
+    sk, d = 262144, 128
+    q = seeded((1, 16, 4, d), 1801, dtype=dtype)
+    k = seeded((1, 1, sk, d), 1802, dtype=dtype)
+    v = seeded((1, 1, sk, d), 1803, dtype=dtype)
+    out, lse = attention_forward(q, k, v, causal=False, scale=1 / math.sqrt(d))
+    eo, el = reference_fp32(q, k, v, causal=False)
+    assert_close(out, eo, **FWD_TOL[dtype], what="O")
+    assert_close(lse, el, **FWD_TOL[dtype], what="LSE")
+    big_k = torch.zeros((1, 1, sk + 1000, d), device="cuda", dtype=dtype)
+    big_v = torch.full((1, 1, sk + 1000, d), float("nan"), device="cuda", dtype=dtype)
+    big_k[:, :, :sk] = k
+    big_v[:, :, :sk] = v
+    out2 = attention(q, big_k[:, :, :sk], big_v[:, :, :sk], causal=False, backend="hip")
+    assert torch.equal(out, out2)
