@@ -241,3 +241,15 @@ def test_config3_bf16_gradients_at_stated_bar():
     assert_close(lse, el, **FWD_TOL[BF16], what="cfg3 bf16 LSE")
     for n, a, e in zip(("dQ", "dK", "dV"), ours, exact):
         assert_close(a, e, **bar, what=f"cfg3 bf16 {n} at 1e-2 + 1e-2 |ref|")
+
+
+def test_long_sequence_training_step():
+    """A 16K-token causal GQA step (B=1, Hq=4, Hkv=1, D=128, fp16): 128 key
+    tiles, stream-K shares across many tile rows, against fp32 autograd
+    (q/k/v scaled 0.5 as in config 3)."""
+    s, d = 16384, 128
+    q = seeded((1, 4, s, d), 1901, dtype=F16, scale=0.5)
+    k = seeded((1, 1, s, d), 1902, dtype=F16, scale=0.5)
+    v = seeded((1, 1, s, d), 1903, dtype=F16, scale=0.5)
+    do = seeded((1, 4, s, d), 1904, dtype=F16)
+    _check_grads(q, k, v, do, True, F16, "S=16384")
