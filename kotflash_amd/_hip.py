@@ -155,6 +155,12 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     key = (index, _stream(device))
     buf = _WORKSPACES.get(key)
     if buf is None or buf.numel() < nbytes:
+        if buf is None and len(_WORKSPACES) >= 64:
+            # Callers that make a new stream per call would otherwise grow
+            # this without bound. Dropping the references is safe: torch's
+            # caching allocator only hands a freed block to later work on the
+            # stream it was allocated for.
+            _WORKSPACES.clear()
         buf = torch.empty(max(nbytes, 256), device=torch.device("cuda", index), dtype=torch.uint8)
         _WORKSPACES[key] = buf
     return buf
