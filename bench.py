@@ -364,6 +364,51 @@ def bench_decode_floor(torch, _hip, sk=16384, replays=20):
     return res
 
 
+def bench_issue_rates(torch):
+    """Shader cycles per v_mfma_f32_32x32x16_f16 when each MFMA is followed
+    by 0-8 instructions of one kind (v_fma_f32, v_exp_f32, ds_read_b128,
+    ds_read_b64_tr_b16), or by one LDS read (two transposed ones) or one
+    exponential and N v_fma_f32, one wave on every SIMD: the probe kernel of
+    kotflash_amd/csrc/probe/issue_rate.hip. Cycles are the wave's own
+    s_memtime span per MFMA; the clock is that span over s_memrealtime
+    (100 MHz). Returns None when the probe library is not built."""
+    import ctypes
+    from pathlib import Path
+
+    path = Path(__file__).resolve().parent / "kotflash_amd" / "libkotflash_probe.so"
+    if not path.is_file():
+        return None
+    lib = ctypes.CDLL(str(path))
+    lib.kfp_issue_rate.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                   ctypes.c_void_p, ctypes.c_void_p]
+    lib.kfp_issue_rate.restype = ctypes.c_int
+    lib.kfp_issue_rounds.restype = ctypes.c_int
+    props = torch.cuda.get_device_properties(0)
+    blocks = 4 * props.multi_processor_count  # one wave per SIMD
+    sink = torch.empty(blocks * 64, device="cuda", dtype=torch.float32)
+    ticks = torch.zeros(blocks * 2, device="cuda", dtype=torch.int64)
+    st = torch.cuda.current_stream().cuda_stream
+    mfmas = 2 * lib.kfp_issue_rounds()
+    kinds = {"v_fma_f32": 0, "v_exp_f32": 1, "ds_read_b128": 2, "ds_read_b64_tr_b16": 3,
+             "ds_read_b128 + N v_fma_f32": 4, "2 ds_read_b64_tr_b16 + N v_fma_f32": 5,
+             "v_exp_f32 + N v_fma_f32": 6}
+    res = {"waves_per_simd": 1, "workgroups": blocks}
+    for name, kind in kinds.items():
+        row = {}
+        for nv in (0, 2, 3, 4, 5, 6, 8):
+            for _ in range(2):  # the second launch is the one read (warm clocks)
+                if lib.kfp_issue_rate(kind, nv, blocks, sink.data_ptr(), ticks.data_ptr(), st):
+                    raise RuntimeError("kfp_issue_rate failed")
+            t = ticks.view(blocks, 2).double().mean(0).tolist()
+            row[str(nv)] = round(t[0] / mfmas, 1)
+            if name == "v_fma_f32" and nv == 0:
+                res["shader_mhz"] = round(t[0] / t[1] * 100.0)
+        res[name] = row
+    res["note"] = ("shader cycles per MFMA (32x32x16 f16, two independent accumulators) with "
+                   "N instructions of the kind after each MFMA, keyed by N")
+    return res
+
+
 def bench_config5(torch, _hip, steps=64, seed=500):
     """cache [8, 8, 32768, 64] fp16 with per-sequence
     lengths U[4096, 28000] (seeded); each of `steps` steps appends n in
@@ -651,6 +696,9 @@ def main() -> int:
     ap.add_argument("--decode-floor", action="store_true",
                     help="run only the config 2 decode floor probes beside the decode (graph "
                          "replays) for a kernel trace and exit (prints no bench line)")
+    ap.add_argument("--issue-rates", action="store_true",
+                    help="run only the MFMA issue-overlap probe (one wave per SIMD) and exit "
+                         "(prints no bench line)")
     ap.add_argument("--only-config5", action="store_true",
                     help="run only the config 5 append/decode loops (two-launch and fused) for "
                          "a kernel trace and exit (prints no bench line)")
@@ -684,6 +732,9 @@ def main() -> int:
         return 0
     if args.decode_floor:
         log(json.dumps(bench_decode_floor(torch, _hip)))
+        return 0
+    if args.issue_rates:
+        log(json.dumps(bench_issue_rates(torch)))
         return 0
 
     ms, wall_ms, dkdv_live, per, work, step_flops, prewarm_steps = bench_train(
