@@ -391,7 +391,8 @@ def bench_issue_rates(torch):
     mfmas = 2 * lib.kfp_issue_rounds()
     kinds = {"v_fma_f32": 0, "v_exp_f32": 1, "ds_read_b128": 2, "ds_read_b64_tr_b16": 3,
              "ds_read_b128 + N v_fma_f32": 4, "2 ds_read_b64_tr_b16 + N v_fma_f32": 5,
-             "v_exp_f32 + N v_fma_f32": 6}
+             "v_exp_f32 + N v_fma_f32": 6, "s_add_u32": 7, "s_waitcnt (satisfied)": 8,
+             "s_nop 0": 9}
     res = {"waves_per_simd": 1, "workgroups": blocks}
     for name, kind in kinds.items():
         row = {}

@@ -12,7 +12,8 @@
 // Kinds: 0 v_fma_f32, 1 v_exp_f32, 2 ds_read_b128, 3 ds_read_b64_tr_b16;
 // mixed slots, `nv` v_fma_f32 after 4 one ds_read_b128, 5 two
 // ds_read_b64_tr_b16, 6 one v_exp_f32 (the shapes of the attention kernels'
-// MFMA slots). The LDS reads address 16 (or 8) consecutive bytes per lane of
+// MFMA slots); scalar-side instructions, 7 s_add_u32, 8 s_waitcnt
+// lgkmcnt(15) (nothing to wait for), 9 s_nop 0. The LDS reads address 16 (or 8) consecutive bytes per lane of
 // a 1 KB (512 B) block of this workgroup's LDS, every read in bounds.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -47,6 +48,7 @@ __global__ __launch_bounds__(64) void issue_kernel(float* sink, uint64_t* ticks,
   const unsigned a16 = (unsigned)(uintptr_t)&lds[threadIdx.x];
   const unsigned a8 = (unsigned)(uintptr_t)lds + 8u * threadIdx.x;
   const float c = seed * 0.5f;
+  unsigned sreg = 0u;
   const uint64_t t0 = __builtin_amdgcn_s_memtime();
   const uint64_t r0 = __builtin_amdgcn_s_memrealtime();
   for (int it = 0; it < kRounds; ++it) {
@@ -64,12 +66,18 @@ __global__ __launch_bounds__(64) void issue_kernel(float* sink, uint64_t* ticks,
       if constexpr (KIND == 6) asm volatile("v_exp_f32 %0, %0" : "+v"(v[7]));
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
-        if constexpr (KIND == 0 || KIND >= 4)
+        if constexpr (KIND == 0 || (KIND >= 4 && KIND <= 6))
           asm volatile("v_fma_f32 %0, %0, %1, %1" : "+v"(v[KIND == 6 ? j % 7 : j & 7]) : "v"(c));
         else if constexpr (KIND == 1)
           asm volatile("v_exp_f32 %0, %0" : "+v"(v[j & 7]));
         else if constexpr (KIND == 2)
           asm volatile("ds_read_b128 %0, %1" : "+v"(r[j & 7]) : "v"(a16));
+        else if constexpr (KIND == 7)
+          asm volatile("s_add_u32 %0, %0, 1" : "+s"(sreg));
+        else if constexpr (KIND == 8)
+          asm volatile("s_waitcnt lgkmcnt(15)" ::: "memory");
+        else if constexpr (KIND == 9)
+          asm volatile("s_nop 0");
         else
           asm volatile("ds_read_b64_tr_b16 %0, %1" : "+v"(*reinterpret_cast<uint64_t*>(&r[j & 7])) : "v"(a8));
       }
@@ -85,7 +93,7 @@ __global__ __launch_bounds__(64) void issue_kernel(float* sink, uint64_t* ticks,
   for (int i = 0; i < 8; ++i) s += v[i] + (float)r[i][0] + (float)r[i][1];
 #pragma unroll
   for (int i = 0; i < 16; ++i) s += c0[i] + c1[i];
-  sink[blockIdx.x * 64 + threadIdx.x] = s;
+  sink[blockIdx.x * 64 + threadIdx.x] = s + (float)sreg;
   if (threadIdx.x == 0) {
     ticks[2 * blockIdx.x] = t1 - t0;
     ticks[2 * blockIdx.x + 1] = r1 - r0;
@@ -127,6 +135,9 @@ int kfp_issue_rate(int kind, int nv, int blocks, float* sink, uint64_t* ticks, v
     case 4: return (int)launch_kind<4>(nv, blocks, sink, ticks, s);
     case 5: return (int)launch_kind<5>(nv, blocks, sink, ticks, s);
     case 6: return (int)launch_kind<6>(nv, blocks, sink, ticks, s);
+    case 7: return (int)launch_kind<7>(nv, blocks, sink, ticks, s);
+    case 8: return (int)launch_kind<8>(nv, blocks, sink, ticks, s);
+    case 9: return (int)launch_kind<9>(nv, blocks, sink, ticks, s);
     default: return (int)hipErrorInvalidValue;
   }
 }
