@@ -536,12 +536,105 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
     for (int db = 0; db < NDB; ++db) asm volatile("" : "+v"(trb2[db][0]), "+v"(trb2[db][1]));
   }
 
+  // Per-lane DMA plan, the same for every unit: for each of this wave's NQI
+  // 1 KB blocks of a tile, the byte offset of this lane's 16-byte chunk
+  // within the tile's rows (kOOB when the chunk is head-dim padding). A unit
+  // adds its first row's offset as the (scalar) soffset; rows past Sq then
+  // fall beyond the resource extent and load as zeros.
+  uint32_t dma_qoff[NQI], dma_doff[NQI];
+#pragma unroll
+  for (int k = 0; k < NQI; ++k) {
+    const int pc = (wave * NQI + k) * 64 + lane;  // physical chunk this lane fills
+    const int r = pc / CPR;
+    const int c = (pc % CPR) ^ Tile::key(r);
+    const bool ok = c * 8 < p.D;
+    dma_qoff[k] = ok ? (uint32_t)(r * p.q_ss + c * 8) * 2u : kOOB;
+    dma_doff[k] = ok ? (uint32_t)(r * p.do_ss + c * 8) * 2u : kOOB;
+  }
+  // Statistics rows: wave 0 loads LSE * log2(e), wave 1 -delta; waves 2 and
+  // 3 load zeros into the unused rows.
+  const uint32_t dma_soff = wave < 2 ? (uint32_t)lane * 4u : kOOB;
+  // LDS byte addresses (M0) of stage 0's blocks for this wave.
+  const uint32_t lds_q0 = lds_addr(&stage[0][0][0]) + (uint32_t)(wave * NQI) * 1024u;
+  const uint32_t lds_s0 = lds_addr(&rowstat[0][0][0]) + (uint32_t)wave * (kBMQ * 4u);
+  constexpr uint32_t kStatBytes = 4u * kBMQ * 4u;
+  const uint32_t q_ext = rows_extent(p.Sq, p.q_ss, p.D);
+  const uint32_t do_ext = rows_extent(p.Sq, p.do_ss, p.D);
+  // Units of a segment are walked in order (query head g, query tile qt
+  // descending): workgroups that start a tile row together read the same
+  // Q/dO tiles at the same time. `Walk` advances one unit without divisions,
+  // and carries the row pointers of head kvh G + g, stepped when g changes,
+  // so that a unit's DMA set-up needs no 64-bit products.
+  struct Walk {
+    int g, qt;
+    int qs, nq;          // the segment's first query tile and query-tile count
+    const uint16_t* qp;  // Q rows of the head
+    const uint16_t* dp;  // dO rows
+    const float* sp;     // statistics rows: LSE log2(e) (wave 0), -delta (wave 1)
+  };
+  auto walk_init = [&](int b, int kvh, int qs, int nq, int it) {
+    Walk w;
+    const int h0 = kvh * p.G;
+    w.g = it / nq;
+    w.qt = qs + nq - 1 - (it - w.g * nq);
+    w.qs = qs;
+    w.nq = nq;
+    w.qp = p.q + b * p.q_sb + (int64_t)(h0 + w.g) * p.q_sh;
+    w.dp = p.dout + b * p.do_sb + (int64_t)(h0 + w.g) * p.do_sh;
+    w.sp = (wave == 0 ? p.lse2 : p.delta) + ((int64_t)b * p.Hq + h0 + w.g) * p.Sq;
+    return w;
+  };
+  auto walk_next = [&](Walk& w) {
+    if (--w.qt < w.qs) {
+      w.qt = w.qs + w.nq - 1;
+      ++w.g;
+      w.qp += p.q_sh;
+      w.dp += p.do_sh;
+      w.sp += p.Sq;
+    }
+  };
+  constexpr int NDMA = 2 * NQI + 1;  // DMA instructions per unit (the last: LSE or delta rows)
+  struct Dma {
+    __amdgpu_buffer_rsrc_t qr, dor, sr;
+    uint32_t qso, dso, sso;  // soffsets: the unit's first row
+    uint32_t lq, ls;         // M0 of this wave's first Q block and of its statistics row
+  };
+  // A unit past the segment's end gets empty resources (no load reaches
+  // memory, whatever the base): its loads then only deposit zeros into the
+  // (free) stage, which keeps the issue unconditional.
+  auto dma_setup = [&](const Walk& w, int st, bool real) {
+    Dma d;
+    const int q0 = real ? w.qt * kBMQ : 0;
+    d.qr = make_rsrc(w.qp, real ? q_ext : 0u);
+    d.dor = make_rsrc(w.dp, real ? do_ext : 0u);
+    d.sr = make_rsrc(w.sp, real ? (uint32_t)p.Sq * 4u : 0u);
+    d.qso = (uint32_t)(q0 * p.q_ss) * 2u;
+    d.dso = (uint32_t)(q0 * p.do_ss) * 2u;
+    d.sso = (uint32_t)q0 * 4u;
+    d.lq = lds_q0 + (uint32_t)st * kStageBytes;
+    d.ls = lds_s0 + (uint32_t)st * kStatBytes;
+    return d;
+  };
+  // DMA instruction j of a unit: Q / dO blocks, then the row statistics.
+  auto dma_issue = [&](const Dma& d, int j) {
+    if (j < 2 * NQI) {
+      const int k = j >> 1;
+      if ((j & 1) == 0)
+        dma16_s(d.qr, d.lq + (uint32_t)k * 1024u, dma_qoff[k], d.qso);
+      else
+        dma16_s(d.dor, d.lq + (uint32_t)(QT * 2) + (uint32_t)k * 1024u, dma_doff[k], d.dso);
+    } else {
+      dma4_s(d.sr, d.ls, dma_soff, d.sso);
+    }
+  };
+
+  // Segments: the tile row (grp, kt) holding unit u, of which this share
+  // covers units [ua, ub) (row-relative).
   const int64_t group_units = p.units / p.ngroups;
   int grp = (int)(u / group_units);
   int kt = 0;
   int64_t row_base = grp * group_units;  // first unit of tile row (grp, kt)
-  bool first_seg = true;
-  while (u < uend) {
+  auto seek = [&]() {
     for (;;) {
       const int64_t row_units = (int64_t)p.G * dkdv_nq(kt, p.nqt, CAUSAL);
       if (u < row_base + row_units) break;
@@ -551,6 +644,46 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
         ++grp;
       }
     }
+  };
+  // A segment's set-up loads: this wave's K and V rows as B operands (lane =
+  // key, slots = head_dim) and the ring's first two units. Both go out
+  // together, and for every segment after the first they go out before the
+  // previous segment's flush, so that their latency overlaps its stores.
+  u32x4 kf[NKS], vf[NKS];
+  Walk wcur, wdma;
+  auto segment_loads = [&]() {
+    const int nq = dkdv_nq(kt, p.nqt, CAUSAL);
+    const int qs = dkdv_qstart(kt, CAUSAL);
+    const int per_tile = p.G * nq;
+    const int ua = (int)(u - row_base);
+    const int ub = (int)min((int64_t)per_tile, ua + (uend - u));
+    const int b = grp / p.Hkv, kvh = grp % p.Hkv;
+    const int key = kt * kBNK + wave * 32 + l32;
+    const bool key_ok = key < p.Sk;
+    const auto kr = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, rows_extent(p.Sk, p.k_ss, p.D));
+    const auto vr = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, rows_extent(p.Sk, p.v_ss, p.D));
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d = 16 * ks + 8 * h32;
+      const bool ok = key_ok && d < p.D;
+      kf[ks] = buf_load16(kr, ok ? (uint32_t)(key * p.k_ss + d) * 2u : kOOB);
+      vf[ks] = buf_load16(vr, ok ? (uint32_t)(key * p.v_ss + d) * 2u : kOOB);
+    }
+    wcur = walk_init(b, kvh, qs, nq, ua);
+    wdma = wcur;
+    const Dma d0 = dma_setup(wdma, 0, true);
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) dma_issue(d0, j);
+    walk_next(wdma);
+    const Dma d1 = dma_setup(wdma, 1, ua + 1 < ub);
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) dma_issue(d1, j);
+    walk_next(wdma);
+  };
+  seek();
+  segment_loads();
+  bool first_seg = true;
+  for (;;) {
     const int nq = dkdv_nq(kt, p.nqt, CAUSAL);
     const int qs = dkdv_qstart(kt, CAUSAL);
     const int per_tile = p.G * nq;
@@ -561,125 +694,18 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
     const int kw0 = k0 + wave * 32;  // first key of this wave
     const int key = kw0 + l32;
     const bool key_ok = key < p.Sk;
+    (void)nq;
+    (void)qs;
 
-    // Stages of the previous segment (and its flush stores) are done with.
+    // This segment's K/V rows and first two units have landed, and every
+    // wave is done with the previous segment's stages and flush.
     wait_all_memory();
     __syncthreads();
-
-    // This wave's K and V rows as B operands: lane = key, slots = head_dim.
-    u32x4 kf[NKS], vf[NKS];
-    {
-      const auto kr = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, rows_extent(p.Sk, p.k_ss, p.D));
-      const auto vr = make_rsrc(p.v + b * p.v_sb + kvh * p.v_sh, rows_extent(p.Sk, p.v_ss, p.D));
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        const int d = 16 * ks + 8 * h32;
-        const bool ok = key_ok && d < p.D;
-        kf[ks] = buf_load16(kr, ok ? (uint32_t)(key * p.k_ss + d) * 2u : kOOB);
-        vf[ks] = buf_load16(vr, ok ? (uint32_t)(key * p.v_ss + d) * 2u : kOOB);
-      }
-    }
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       dk[db] = zero16();
       dv[db] = zero16();
     }
-    // K/V fragments are in registers before the ring starts: the ring's own
-    // loads are waited for explicitly below, and any compiler-inserted wait
-    // on these fragments inside the loop would also drain the ring.
-    wait_all_memory();
-
-    // Per-lane DMA plan, fixed for the segment: for each of this wave's NQI
-    // 1 KB blocks of a tile, the byte offset of this lane's 16-byte chunk
-    // within the tile's rows (kOOB when the chunk is head-dim padding). A
-    // unit adds its first row's offset as the (scalar) soffset; rows past Sq
-    // then fall beyond the resource extent and load as zeros.
-    uint32_t dma_qoff[NQI], dma_doff[NQI];
-#pragma unroll
-    for (int k = 0; k < NQI; ++k) {
-      const int pc = (wave * NQI + k) * 64 + lane;  // physical chunk this lane fills
-      const int r = pc / CPR;
-      const int c = (pc % CPR) ^ Tile::key(r);
-      const bool ok = c * 8 < p.D;
-      dma_qoff[k] = ok ? (uint32_t)(r * p.q_ss + c * 8) * 2u : kOOB;
-      dma_doff[k] = ok ? (uint32_t)(r * p.do_ss + c * 8) * 2u : kOOB;
-    }
-    // Statistics rows: wave 0 loads LSE * log2(e), wave 1 -delta; waves 2 and
-    // 3 load zeros into the unused rows.
-    const uint32_t dma_soff = wave < 2 ? (uint32_t)lane * 4u : kOOB;
-    // LDS byte addresses (M0) of stage 0's blocks for this wave.
-    const uint32_t lds_q0 = lds_addr(&stage[0][0][0]) + (uint32_t)(wave * NQI) * 1024u;
-    const uint32_t lds_s0 = lds_addr(&rowstat[0][0][0]) + (uint32_t)wave * (kBMQ * 4u);
-    constexpr uint32_t kStatBytes = 4u * kBMQ * 4u;
-    // Units are walked in order (query head g, query tile qt descending):
-    // workgroups that start a tile row together read the same Q/dO tiles at
-    // the same time. `Walk` advances one unit without divisions, and carries
-    // the row pointers of head kvh G + g, stepped when g changes, so that a
-    // unit's DMA set-up needs no 64-bit products.
-    struct Walk {
-      int g, qt;
-      const uint16_t* qp;  // Q rows of the head
-      const uint16_t* dp;  // dO rows
-      const float* sp;     // statistics rows: LSE log2(e) (wave 0), -delta (wave 1)
-    };
-    const int h0 = kvh * p.G;
-    const uint16_t* q_h0 = p.q + b * p.q_sb + (int64_t)h0 * p.q_sh;
-    const uint16_t* do_h0 = p.dout + b * p.do_sb + (int64_t)h0 * p.do_sh;
-    const float* st_h0 = (wave == 0 ? p.lse2 : p.delta) + ((int64_t)b * p.Hq + h0) * p.Sq;
-    const uint32_t q_ext = rows_extent(p.Sq, p.q_ss, p.D);
-    const uint32_t do_ext = rows_extent(p.Sq, p.do_ss, p.D);
-    auto walk_init = [&](int it) {
-      Walk w;
-      w.g = it / nq;
-      w.qt = qs + nq - 1 - (it - w.g * nq);
-      w.qp = q_h0 + (int64_t)w.g * p.q_sh;
-      w.dp = do_h0 + (int64_t)w.g * p.do_sh;
-      w.sp = st_h0 + (int64_t)w.g * p.Sq;
-      return w;
-    };
-    auto walk_next = [&](Walk& w) {
-      if (--w.qt < qs) {
-        w.qt = qs + nq - 1;
-        ++w.g;
-        w.qp += p.q_sh;
-        w.dp += p.do_sh;
-        w.sp += p.Sq;
-      }
-    };
-    constexpr int NDMA = 2 * NQI + 1;  // DMA instructions per unit (the last: LSE or delta rows)
-    struct Dma {
-      __amdgpu_buffer_rsrc_t qr, dor, sr;
-      uint32_t qso, dso, sso;  // soffsets: the unit's first row
-      uint32_t lq, ls;         // M0 of this wave's first Q block and of its statistics row
-    };
-    // A unit past the segment's end gets empty resources (no load reaches
-    // memory, whatever the base): its loads then only deposit zeros into the
-    // (free) stage, which keeps the issue unconditional.
-    auto dma_setup = [&](const Walk& w, int st, bool real) {
-      Dma d;
-      const int q0 = real ? w.qt * kBMQ : 0;
-      d.qr = make_rsrc(w.qp, real ? q_ext : 0u);
-      d.dor = make_rsrc(w.dp, real ? do_ext : 0u);
-      d.sr = make_rsrc(w.sp, real ? (uint32_t)p.Sq * 4u : 0u);
-      d.qso = (uint32_t)(q0 * p.q_ss) * 2u;
-      d.dso = (uint32_t)(q0 * p.do_ss) * 2u;
-      d.sso = (uint32_t)q0 * 4u;
-      d.lq = lds_q0 + (uint32_t)st * kStageBytes;
-      d.ls = lds_s0 + (uint32_t)st * kStatBytes;
-      return d;
-    };
-    // DMA instruction j of a unit: Q / dO blocks, then the row statistics.
-    auto dma_issue = [&](const Dma& d, int j) {
-      if (j < 2 * NQI) {
-        const int k = j >> 1;
-        if ((j & 1) == 0)
-          dma16_s(d.qr, d.lq + (uint32_t)k * 1024u, dma_qoff[k], d.qso);
-        else
-          dma16_s(d.dor, d.lq + (uint32_t)(QT * 2) + (uint32_t)k * 1024u, dma_doff[k], d.dso);
-      } else {
-        dma4_s(d.sr, d.ls, dma_soff, d.sso);
-      }
-    };
 
     // One unit: both 32-row query blocks (qb) of the staged tile against this
     // wave's 32 keys, with the causal mask (key <= row) on blocks that cross
@@ -858,17 +884,6 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
     // flight; wait for those of `it` (this wave's), then the barrier makes
     // every wave's loads visible and frees the stage of unit it - 1, which
     // receives unit it + 2 (issued from inside the unit's first phase).
-    Walk wcur = walk_init(ua), wdma = wcur;
-    {
-      const Dma d0 = dma_setup(wdma, 0, true);
-#pragma unroll
-      for (int j = 0; j < NDMA; ++j) dma_issue(d0, j);
-      walk_next(wdma);
-      const Dma d1 = dma_setup(wdma, 1, ua + 1 < ub);
-#pragma unroll
-      for (int j = 0; j < NDMA; ++j) dma_issue(d1, j);
-      walk_next(wdma);
-    }
     // The loop is unrolled by the ring's NST stages, so that every LDS offset
     // inside a unit is a compile-time constant.
     for (int it0 = ua; it0 < ub; it0 += NST) {
@@ -888,6 +903,15 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
           walk_next(wdma);
         }
       });
+    }
+    // Every wave is done with the ring's stages: the next segment's loads
+    // can go out now, ahead of this segment's flush.
+    __syncthreads();
+    const bool more = u + (ub - ua) < uend;
+    if (more) {
+      u += ub - ua;
+      seek();
+      segment_loads();
     }
 
     // Flush: dK^T / dV^T layout is lane = key, register r = head_dim
@@ -923,8 +947,8 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
         }
       }
     }
-    u += ub - ua;
     first_seg = false;
+    if (!more) break;
   }
 }
 
@@ -1017,9 +1041,10 @@ static size_t delta_bytes(int64_t B, int64_t Hq, int64_t Sq) {
 }
 
 // Cost-weighted stream-K boundaries (see DkdvSplit). A segment start costs
-// kSegmentCost8 / 8 units: on the MI355X at config 3 a segment's fixed cost
-// came out at 2.5 units from per-workgroup timestamps, and a sweep of the
-// weight put the shortest launch at 4.5 to 6 units.
+// kSegmentCost8 / 8 units: on the MI355X at config 3 a sweep of the weight
+// put the shortest launch at 4.5 to 6 units, and after a segment's loads
+// came to overlap the previous segment's flush, 3 and 4 units were still
+// 1-2% slower than 5.
 constexpr int kSegmentCost8 = 40;
 // Returns the number of tile rows that a share boundary cuts (shared tiles).
 static int dkdv_split(DkdvSplit& sp, int ngroups, int G, int nqt, int nkt, bool causal, int nwg) {
