@@ -25,7 +25,7 @@ from .kernels.hip_decode import (  # noqa: F401  strided_decode_supported: the r
     strided_decode_supported,
     validated_decode_supported,
 )
-from .kernels.hip_forward import attention_forward, triton_turing_supported
+from .kernels.hip_forward import attention_forward, forward_validated, triton_turing_supported
 
 BACKENDS = ("auto", "hip", "triton", "sdpa")
 _DTYPE_NAMES = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float32"}
@@ -187,7 +187,7 @@ class _HipAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, causal: bool, scale: float):
-        out, lse = attention_forward(q, k, v, causal=causal, scale=scale)
+        out, lse = forward_validated(q, k, v, causal=causal, scale=scale)
         ctx.save_for_backward(q, k, v, out, lse)
         ctx.causal = causal
         ctx.scale = scale
@@ -216,7 +216,7 @@ def _hip_op_attention(q, k, v, causal: bool, scale: float) -> torch.Tensor:
     if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
         out = _HipAttention.apply(q, k, v, causal, scale)
     else:
-        out = attention_forward(q, k, v, causal=causal, scale=scale)[0]
+        out = forward_validated(q, k, v, causal=causal, scale=scale)[0]
     return out if out.is_contiguous() else out.contiguous()
 
 

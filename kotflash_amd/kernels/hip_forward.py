@@ -48,9 +48,20 @@ def attention_forward(q, k, v, *, causal: bool, scale: float):
     """Run the HIP forward; returns ``(out, lse)``."""
     require_hip_tensors("HIP attention forward", q, k, v)
     _check_shapes(q, k, v)
+    return forward_validated(q, k, v, causal=causal, scale=scale)
+
+
+def forward_validated(q, k, v, *, causal: bool, scale: float):
+    """``attention_forward`` for callers that have already validated q/k/v as
+    ``attention`` does (shapes, one device and dtype, and a HIP route: gfx950,
+    fp16/bf16, 8 <= head_dim <= 128, the library loaded); it skips repeating
+    those checks, which are a sizeable part of a small call's host time."""
     d = q.shape[3]
     dp = padded_head_dim(d)
-    q_, k_, v_ = (prepare(t, dp) for t in (q, k, v))
+    if dp == d and _hip.layout_ok(q) and _hip.layout_ok(k) and _hip.layout_ok(v):
+        q_, k_, v_ = q, k, v
+    else:
+        q_, k_, v_ = prepare(q, dp), prepare(k, dp), prepare(v, dp)
     b, hq, sq, _ = q_.shape
     hkv, sk = k_.shape[1], k_.shape[2]
     out = torch.empty((b, hq, sq, dp), device=q.device, dtype=q.dtype)
