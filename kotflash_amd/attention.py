@@ -19,7 +19,7 @@ import torch.nn.functional as F
 
 from . import _hip
 from ._planning import gfx950_profile_for_shapes, t4_profile_for_shapes
-from .kernels.hip_backward import attention_backward
+from .kernels.hip_backward import attention_backward, backward_validated
 from .kernels.hip_decode import (  # noqa: F401  strided_decode_supported: the reference's module name
     decode_supported_unchecked,
     strided_decode_supported,
@@ -196,9 +196,14 @@ class _HipAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         q, k, v, out, lse = ctx.saved_tensors
-        dq, dk, dv = attention_backward(
-            q, k, v, out, lse, grad_out, causal=ctx.causal, scale=ctx.scale
-        )
+        if grad_out.shape != out.shape or grad_out.dtype != out.dtype or grad_out.device != out.device:
+            dq, dk, dv = attention_backward(
+                q, k, v, out, lse, grad_out, causal=ctx.causal, scale=ctx.scale
+            )
+        else:
+            dq, dk, dv = backward_validated(
+                q, k, v, out, lse, grad_out, causal=ctx.causal, scale=ctx.scale
+            )
         return dq, dk, dv, None, None
 
 

@@ -22,6 +22,14 @@ def attention_backward(q, k, v, out, lse, grad_out, *, causal: bool, scale: floa
         raise ValueError("out and grad_out must have q's shape")
     if lse.shape != q.shape[:3] or lse.dtype != torch.float32:
         raise ValueError("lse must be float32 [B, Hq, Sq]")
+    return backward_validated(q, k, v, out, lse, grad_out, causal=causal, scale=scale)
+
+
+def backward_validated(q, k, v, out, lse, grad_out, *, causal: bool, scale: float):
+    """``attention_backward`` for the autograd path, whose q/k/v/out/lse come
+    from a validated HIP forward and whose grad_out autograd gives out's
+    shape and dtype: it skips repeating those checks (a small step's host
+    time). grad_out's layout is still prepared like every other input."""
     d = q.shape[3]
     dp = padded_head_dim(d)
     q_, k_, v_, o_, do_ = (prepare(t, dp) for t in (q, k, v, out, grad_out))
