@@ -77,9 +77,19 @@ __device__ inline void fwd_map_block(int bid, int nqt, int B, int Hq, int Hkv, i
 // KS is the number of 16-column k-steps of the S = K Q^T contraction: DT / 16,
 // or fewer when the head dim ends earlier inside the tile (D <= 80 in a
 // 96-wide tile needs 5): the skipped columns are zero padding on both sides.
-template <typename T, int DT, int KS, int QB, bool CAUSAL>
-__global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdParams p) {
-  constexpr int BM = 4 * QB * 32;
+//
+// SPLIT (short problems, where 128-row tiles leave most CUs idle): the
+// workgroup owns 32 query rows and its four waves split the key range
+// instead, wave w taking K/V tiles w, w + 4, ... through a ring of its own in
+// LDS (no workgroup barrier per tile). Each wave ends with its own (m, l, O)
+// over its tiles; they are combined through LDS with the LSE weights
+// 2^(m_w - M) / sum_w l_w 2^(m_w - M), as split-KV partials are (reference
+// triton_forward.py:269-349). The longest chain of dependent tiles is a
+// quarter of the unsplit kernel's, and the grid four times as large.
+template <typename T, int DT, int KS, int QB, bool CAUSAL, bool SPLIT>
+__global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? 2 : 1)) void fwd_kernel(const FwdParams p) {
+  static_assert(!SPLIT || QB == 1, "the split form has one 32-row block per workgroup");
+  constexpr int BM = SPLIT ? 32 : 4 * QB * 32;
   constexpr int BN = 64;
   constexpr int CPR = DT / 8;           // 16-byte chunks per row
   constexpr int NKS = KS;               // MFMA k-steps over head_dim
@@ -87,10 +97,21 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
   constexpr int NDB = DT / 32;          // 32-wide head_dim blocks of O^T
   constexpr int TB = BN * DT * 2;       // bytes of one K (or V) tile
   constexpr int STAGE_B = 2 * TB;       // K | V
-  constexpr int NKI = BN * CPR / 256;   // 1 KB loads per wave per tile and matrix
-  static_assert(BN * CPR == 256 * NKI, "tile chunks must split into whole loads");
+  // Ring stages: two, shared by the workgroup; in the split form one ring per
+  // wave, of two stages where four of them fit the LDS (head dims up to 64).
+  constexpr int NST = (SPLIT && DT > 64) ? 1 : 2;
+  // 1 KB loads per wave per tile and matrix: a quarter of the tile, or all of
+  // it in the split form.
+  constexpr int NKI = BN * CPR / (SPLIT ? 64 : 256);
+  static_assert(BN * CPR == (SPLIT ? 64 : 256) * NKI, "tile chunks must split into whole loads");
+  constexpr int RING_B = (SPLIT ? 4 : 1) * NST * STAGE_B;
+  // Split form: the merge buffer (per wave O^T rows padded to DT + 1 floats,
+  // then m and l per row) overlays the rings after the last tile.
+  constexpr int OSTR = DT + 1;
+  constexpr int MERGE_B = SPLIT ? (4 * 32 * OSTR + 2 * 4 * 32) * 4 : 0;
+  constexpr int SMEM_B = RING_B > MERGE_B ? RING_B : MERGE_B;
   using Tile = SwizzledTile<CPR>;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE_B / 2];
+  __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM_B / 2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
@@ -100,7 +121,7 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
   fwd_map_block(blockIdx.x, p.nqt, p.B, p.Hq, p.Hkv, qt, b, h);
   const int kvh = h / (p.Hq / p.Hkv);
   const int q0 = qt * BM;
-  const int wq0 = q0 + wave * QB * 32;
+  const int wq0 = SPLIT ? q0 : q0 + wave * QB * 32;
 
   const auto qr = make_rsrc(p.q + b * p.q_sb + h * p.q_sh, rows_extent(p.Sq, p.q_ss, p.D));
   const auto kr = make_rsrc(p.k + b * p.k_sb + kvh * p.k_sh, rows_extent(p.Sk, p.k_ss, p.D));
@@ -140,6 +161,9 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
 
   const int nkeys = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
   const int ntiles = cdiv(nkeys, BN);
+  // This wave's tiles: all of them, or every fourth from tile `wave`.
+  const int nl = SPLIT ? (ntiles > wave ? (ntiles - wave + 3) / 4 : 0) : ntiles;
+  auto tile_of = [&](int li) { return SPLIT ? wave + 4 * li : li; };
 
   // K/V tiles stream into a two-stage LDS ring by direct-to-LDS loads, stored
   // unpadded with the swizzle of SwizzledTile (conflict-free for both the
@@ -151,23 +175,35 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
   uint32_t koff[NKI], voff[NKI];
 #pragma unroll
   for (int k = 0; k < NKI; ++k) {
-    const int pc = (wave * NKI + k) * 64 + lane;
+    const int pc = ((SPLIT ? 0 : wave * NKI) + k) * 64 + lane;
     const int r = pc / CPR;
     const int c = (pc % CPR) ^ Tile::key(r);
     const bool ok = c * 8 < p.D;
     koff[k] = ok ? (uint32_t)(r * p.k_ss + c * 8) * 2u : kOOB;
     voff[k] = ok ? (uint32_t)(r * p.v_ss + c * 8) * 2u : kOOB;
   }
-  const uint32_t lds0 = lds_addr(smem);
+  const uint32_t lds0 = lds_addr(smem) + (SPLIT ? (uint32_t)(wave * NST * STAGE_B) : 0u);
   auto tile_load = [&](int tile, int st) {
     const uint32_t kso = (uint32_t)(tile * BN * p.k_ss) * 2u;
     const uint32_t vso = (uint32_t)(tile * BN * p.v_ss) * 2u;
-    const uint32_t m0 = lds0 + (uint32_t)st * STAGE_B + (uint32_t)(wave * NKI) * 1024u;
+    const uint32_t m0 = lds0 + (uint32_t)st * STAGE_B + (SPLIT ? 0u : (uint32_t)(wave * NKI) * 1024u);
 #pragma unroll
     for (int k = 0; k < NKI; ++k) {
       dma16_s(kr, m0 + k * 1024u, koff[k], kso);
       dma16_s(vr, m0 + TB + k * 1024u, voff[k], vso);
     }
+  };
+  // The one-stage ring of the split form loads a tile's K and V separately,
+  // each once the previous tile's reads of it are done.
+  auto tile_load_k = [&](int tile) {
+    const uint32_t kso = (uint32_t)(tile * BN * p.k_ss) * 2u;
+#pragma unroll
+    for (int k = 0; k < NKI; ++k) dma16_s(kr, lds0 + k * 1024u, koff[k], kso);
+  };
+  auto tile_load_v = [&](int tile) {
+    const uint32_t vso = (uint32_t)(tile * BN * p.v_ss) * 2u;
+#pragma unroll
+    for (int k = 0; k < NKI; ++k) dma16_s(vr, lds0 + TB + k * 1024u, voff[k], vso);
   };
   // LDS read bases (bytes, stage 0, key block 0). K rows for S^T: lane row
   // l32, logical chunk 2 ks + h32. V^T transposed reads: the lo / hi rows
@@ -189,19 +225,23 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
       }
   }
 
-  if (ntiles > 0) tile_load(0, 0);
+  if (nl > 0) tile_load(tile_of(0), 0);
   wait_all_memory();
-  __syncthreads();
+  if constexpr (!SPLIT) __syncthreads();
 
-  // One tile on ring stage ST (a compile-time constant, so every LDS offset
-  // in the body is an immediate).
-  auto tile_body = [&](int it, auto stc) {
+  // This wave's li-th tile on ring stage ST (a compile-time constant, so
+  // every LDS offset in the body is an immediate).
+  auto tile_body = [&](int li, auto stc) {
     constexpr int ST = decltype(stc)::value;
-    if (it + 1 < ntiles) tile_load(it + 1, ST ^ 1);
-    const int kbase = it * BN;
+    if constexpr (NST == 2) {
+      if (li + 1 < nl) tile_load(tile_of(li + 1), ST ^ 1);
+    }
+    const int kbase = tile_of(li) * BN;
     // A causal tile whose first key is beyond every row of the wave is fully
-    // masked for it.
-    const bool active = !CAUSAL || kbase <= wq0 + QB * 32 - 1;
+    // masked for it. The split form's tiles all hold visible keys (its
+    // ntiles ends at the block's last row), and its one-stage ring relies on
+    // every tile body issuing the next tile's loads.
+    const bool active = SPLIT || !CAUSAL || kbase <= wq0 + QB * 32 - 1;
     if (active) {
       // S^T = K Q^T as a stream of 2 NKS MFMA slots (key block kb = m / NKS,
       // k-step ks = m % NKS); each slot also issues the LDS read of the
@@ -244,11 +284,23 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
         for (int qb = 0; qb < QB; ++qb)
           s[qb][m / NKS] = Elem<T>::mfma(kop[m], qf[qb][m % NKS], s[qb][m / NKS]);
         if constexpr (m + LA < NS) read_k(m + LA);
-        else if constexpr (m + LA - NS < NPV) read_v(m + LA - NS);
+        else if constexpr (m + LA - NS < NPV) {
+          // One stage: this tile's V was loaded after the previous tile's PV.
+          if constexpr (NST == 1 && m + LA == NS) KF_WAIT_VMCNT(0);
+          read_v(m + LA - NS);
+        }
         __builtin_amdgcn_sched_barrier(0);
       });
 
       __builtin_amdgcn_s_setprio(0);
+      if constexpr (NST == 1) {
+        // Every K read of this tile fed an S product: the next K can land
+        // while the softmax and the PV product run.
+        if (li + 1 < nl) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          tile_load_k(tile_of(li + 1));
+        }
+      }
       const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && kbase + BN - 1 > wq0);
       u32x4 pk[QB][4];
 #pragma unroll
@@ -321,12 +373,97 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
       });
       __builtin_amdgcn_s_setprio(0);
     }
-    KF_WAIT_VMCNT(0);  // this wave's loads of the next tile
-    __syncthreads();   // every wave's loads landed; stage ST is free again
+    if constexpr (NST == 1) {
+      // Every V read fed a PV product: the next V lands during the next S
+      // product.
+      if (li + 1 < nl) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        tile_load_v(tile_of(li + 1));
+      }
+    }
+    // This wave's loads of the next tile (one stage: its K; its V is waited
+    // for before the first V read).
+    KF_WAIT_VMCNT(NST == 1 ? NKI : 0);
+    // Every wave's loads landed; stage ST is free again. The split form's
+    // rings are per wave, and the wave's own wait suffices.
+    if constexpr (!SPLIT) __syncthreads();
   };
-  for (int it = 0; it < ntiles; it += 2) {
-    tile_body(it, std::integral_constant<int, 0>{});
-    if (it + 1 < ntiles) tile_body(it + 1, std::integral_constant<int, 1>{});
+  if constexpr (NST == 2) {
+    for (int li = 0; li < nl; li += 2) {
+      tile_body(li, std::integral_constant<int, 0>{});
+      if (li + 1 < nl) tile_body(li + 1, std::integral_constant<int, 1>{});
+    }
+  } else {
+    for (int li = 0; li < nl; ++li) tile_body(li, std::integral_constant<int, 0>{});
+  }
+
+  if constexpr (SPLIT) {
+    // Merge the four waves' (m, l, O) of the same 32 rows. The buffer
+    // overlays the other waves' rings, hence the barrier first.
+    __syncthreads();
+    float* ob = reinterpret_cast<float*>(smem);  // [wave][row][OSTR]
+    float* mb = ob + 4 * 32 * OSTR;              // [wave][row]
+    float* lb = mb + 4 * 32;                     // [wave][row]
+    {
+      const float lt = wave_xor32_sum(l_i[0]);
+      float* orow = ob + (wave * 32 + l32) * OSTR;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) orow[32 * db + 8 * (r >> 2) + 4 * h32 + (r & 3)] = oacc[0][db][r];
+      if (h32 == 0) {
+        mb[wave * 32 + l32] = m_i[0];
+        lb[wave * 32 + l32] = lt;
+      }
+    }
+    __syncthreads();
+    // Wave w stores head-dim columns [w DT/4, (w + 1) DT/4) of the 32 rows;
+    // a lane takes row l32 and half h32 of those columns.
+    constexpr int CW = DT / 4, CH = CW / 2;
+    static_assert(CH % 4 == 0, "stores are 4 columns wide");
+    const int row = l32;
+    float mw[4], M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      mw[w] = mb[w * 32 + row];
+      M = fmaxf(M, mw[w]);
+    }
+    float sc[4], L = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      // A wave with no tile (or only masked keys) for this row has m = -inf
+      // and weight 0.
+      sc[w] = mw[w] == kNegInf ? 0.f : fast_exp2(mw[w] - M);
+      L += lb[w * 32 + row] * sc[w];
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) sc[w] *= inv;
+    const int qrow = q0 + row;
+    if (qrow < p.Sq) {
+      uint16_t* Op = p.o + b * p.o_sb + h * p.o_sh + qrow * p.o_ss;
+      const int c0 = wave * CW + h32 * CH;
+#pragma unroll
+      for (int j = 0; j < CH; j += 4) {
+        const int d = c0 + j;
+        if (d < p.D) {
+          float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const float* src = ob + (w * 32 + row) * OSTR + d;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = fmaf(src[e], sc[w], o[e]);
+          }
+          u32x2 wv;
+          wv[0] = pack2<T>(o[0], o[1]);
+          wv[1] = pack2<T>(o[2], o[3]);
+          *reinterpret_cast<u32x2*>(Op + d) = wv;
+        }
+      }
+      if (wave == 0 && h32 == 0)
+        p.lse[((int64_t)b * p.Hq + h) * p.Sq + qrow] = L > 0.f ? (M + fast_log2(L)) * kLn2 : kNegInf;
+    }
+    return;
   }
 
 #pragma unroll
@@ -357,17 +494,40 @@ __global__ __launch_bounds__(256, (QB == 1 ? 2 : 1)) void fwd_kernel(const FwdPa
   }
 }
 
+// The split form runs when a grid of 128-row tiles would leave most of the
+// 256 CUs idle and a tile sees more than two K/V tiles: config 1's 64
+// workgroups, for instance, become 256 with chains of at most two tiles. Its
+// grid (four times the tiles, one workgroup per CU) fits one round of the
+// CUs up to 64 tiles; causal grids, whose tiles differ in length, still gain
+// up to 128. Measured on MI355X against the tiled form: config 1 -37%;
+// 256 tiles or non-causal D >= 96 at 96-128 tiles run 5-20% slower split.
+constexpr int64_t kFwdSplitMaxTiles = 64;
+constexpr int64_t kFwdSplitMaxTilesCausal = 128;
+
+static bool fwd_use_split(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, bool causal) {
+  const int64_t tiles = (Sq + 127) / 128 * B * Hq;
+  return Sk > 128 && tiles <= (causal ? kFwdSplitMaxTilesCausal : kFwdSplitMaxTiles);
+}
+
 template <typename T, int DT, int KS, int QB>
 static int launch_fwd(const FwdParams& prm, bool causal, hipStream_t stream) {
   FwdParams p = prm;
-  constexpr int BM = 4 * QB * 32;
+  const bool split = QB == 1 && fwd_use_split(p.B, p.Hq, p.Sq, p.Sk, causal);
+  const int BM = split ? 32 : 4 * QB * 32;
   p.nqt = cdiv(p.Sq, BM);
   const int64_t grid = (int64_t)p.nqt * p.B * p.Hq;
   if (grid > 0x7fffffff) return set_error(KF_EUNSUPPORTED, "kf_attn_fwd: grid too large");
-  if (causal)
-    hipLaunchKernelGGL((fwd_kernel<T, DT, KS, QB, true>), dim3((unsigned)grid), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL((fwd_kernel<T, DT, KS, QB, false>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  const dim3 g((unsigned)grid), blk(256);
+  if (split) {
+    if (causal)
+      hipLaunchKernelGGL((fwd_kernel<T, DT, KS, 1, true, true>), g, blk, 0, stream, p);
+    else
+      hipLaunchKernelGGL((fwd_kernel<T, DT, KS, 1, false, true>), g, blk, 0, stream, p);
+  } else if (causal) {
+    hipLaunchKernelGGL((fwd_kernel<T, DT, KS, QB, true, false>), g, blk, 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((fwd_kernel<T, DT, KS, QB, false, false>), g, blk, 0, stream, p);
+  }
   return check_launch("kf_attn_fwd");
 }
 

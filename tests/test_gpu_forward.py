@@ -80,6 +80,33 @@ def test_forward_edge_shapes(shape):
     assert_close(lse, el, **FWD_TOL[F16], what=f"LSE {shape}")
 
 
+@pytest.mark.parametrize("shape", [
+    # (B, Hq, Hkv, Sq, Sk, D, causal, dtype). The launcher takes the split
+    # form (four waves share a 32-row block's key range) while Sk > 128 and
+    # B * Hq * ceil(Sq / 128) <= 128 (causal) or 64 (non-causal), the 128-row
+    # tiled form otherwise; ragged edges on both sides of that line.
+    (1, 128, 32, 100, 300, 64, True, F16),     # split, at the causal limit
+    (1, 129, 43, 100, 300, 64, True, F16),     # tiled, one tile past it
+    (2, 20, 4, 300, 257, 128, True, F16),      # split, one-stage rings, Sq > Sk
+    (2, 40, 8, 257, 300, 128, True, F16),      # tiled, Sq < Sk
+    (2, 40, 8, 257, 200, 96, False, F16),      # tiled, Sq > Sk
+    (1, 8, 2, 1000, 1000, 32, True, F16),      # split, 32-wide tile
+    (1, 32, 8, 129, 1100, 64, False, F16),     # split, at the limit; waves of 4-5 tiles
+    (1, 33, 11, 129, 1100, 64, False, F16),    # tiled, one tile past it
+    (1, 8, 2, 700, 700, 128, True, BF16),      # split, bf16
+    (1, 6, 3, 90, 1000, 72, False, BF16),      # split, 96-wide tile with 5 k-steps
+])
+def test_forward_split_and_tiled_forms(shape):
+    b, hq, hkv, sq, sk, d, causal, dtype = shape
+    q = seeded((b, hq, sq, d), 24, dtype=dtype)
+    k = seeded((b, hkv, sk, d), 25, dtype=dtype)
+    v = seeded((b, hkv, sk, d), 26, dtype=dtype)
+    out, lse = attention_forward(q, k, v, causal=causal, scale=1 / math.sqrt(d))
+    eo, el = reference_fp32(q, k, v, causal=causal)
+    assert_close(out, eo, **FWD_TOL[dtype], what=f"O {shape}")
+    assert_close(lse, el, **FWD_TOL[dtype], what=f"LSE {shape}")
+
+
 def test_forward_reads_strided_views_in_place():
     """q/k/v as [B, S, H, D] storage viewed as [B, H, S, D] (no copy)."""
     base_q = seeded((2, 200, 8, 64), 31, dtype=F16)
