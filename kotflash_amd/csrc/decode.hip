@@ -613,9 +613,13 @@ extern "C" int kf_decode_num_splits(int64_t B, int64_t Hq, int64_t Hkv, int64_t 
   return (int)ns;
 }
 
-// Ragged batches: workgroups the planner aims for (about four per CU), so
-// that short sequences' splits and long ones' even out across the CUs.
-constexpr int64_t kDecRaggedWGs = 1024;
+// Ragged batches: non-empty workgroups the planner aims for. Swept on MI355X
+// over 256-1024 at config 5's shapes (B=8, Hkv=8, Hq=32, n = 1-16 new rows
+// per step) for three length spreads (1K-8K, 4K-28K, 16K-31K): 384 was the
+// fastest or within 0.4% of it in each, 5-9% ahead of 1024, whose smaller
+// chunks write and merge more fp32 partials; 448 and 512 were not monotone
+// in between (up to 14% behind 384).
+constexpr int64_t kDecRaggedWGs = 384;
 
 static int64_t decode_row_blocks(int64_t G, int64_t Sq) {
   const int rb = decode_rows_per_wg(G, Sq);
