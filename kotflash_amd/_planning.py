@@ -111,8 +111,9 @@ def gfx950_decode_eligible(sq: int, sk: int, d: int, *, causal: bool) -> bool:
 # whose launch and autograd paths are C++, finishes first. Measured on MI355X
 # through the public API (python -m kotflash_amd.benchmark, B=2 Hq=8 Hkv=2
 # D=64 causal, fp16; fwd+bwd us, HIP vs SDPA):
-#   S=256: 253 vs 188;  S=512: 243 vs 185;  S=1024: 248 vs 263;
-#   S=2048: 261 vs 411;  B=1 H=8 S=512 D=128 non-causal (1.1e9 FLOP): 250 vs 175.
+#   S=256: 220 vs 183;  S=512: 216 vs 179;  S=1024: 213 vs 262;
+#   S=2048: 261 vs 411 (an earlier run);  B=1 H=8 S=512 D=128 non-causal
+#   (1.1e9 FLOP): 215 vs 174.
 # Inference calls (no backward to follow) are not subject to it: the HIP
 # forward's launch path is the shorter one (config 1, S=512: 18.9 us per call
 # against 22.4 us for SDPA, bench.py torch_sdpa_same_gpu), and split-KV decode
