@@ -102,12 +102,13 @@ def _sdpa(q, k, v, *, causal: bool, scale: Optional[float]):
 @lru_cache(maxsize=8)
 def _is_measured_t4_runtime(device_index: int) -> bool:
     """The reference's exact-stack T4 gate (kotflash/attention.py:74-87). It
-    requires CUDA 12.4 on a Tesla T4, so it is False on every ROCm stack."""
+    requires CUDA 12.4 on a Tesla T4, so it is False on every ROCm stack. The
+    conditions that need no device query are tested first."""
+    if not triton_turing_supported() or torch.version.cuda != "12.4":
+        return False
     device = torch.device("cuda", device_index)
     return (
         torch.cuda.is_available()
-        and triton_turing_supported()
-        and torch.version.cuda == "12.4"
         and torch.cuda.get_device_capability(device) == (7, 5)
         and torch.cuda.get_device_name(device) == "Tesla T4"
         and torch.__version__.split("+", 1)[0] == "2.6.0"
@@ -122,7 +123,7 @@ def _t4_profile_backend(q, k, v, *, causal: bool, scale: float):
     """Backend for an exact measured T4 shape (reference attention.py:90-106)."""
     if not q.is_cuda or q.dtype != torch.float16:
         return None
-    if not _is_measured_t4_runtime(_device_index(q)):
+    if not triton_turing_supported() or not _is_measured_t4_runtime(_device_index(q)):
         return None
     return t4_profile_for_shapes(
         tuple(q.shape), tuple(k.shape), tuple(v.shape), causal=causal, scale=scale,

@@ -18,6 +18,48 @@ def test_package_exports():
     assert kotflash_amd.hip_available() is False  # no GPU here
 
 
+def test_t4_gate_needs_every_condition(monkeypatch):
+    """The reference's exact-stack T4 gate (kotflash/attention.py:74-87):
+    true only for Triton on SM75 with CUDA 12.4, a Tesla T4 and torch 2.6.0,
+    and false when any one of them differs (it is false on ROCm)."""
+    import importlib
+
+    impl = importlib.import_module("kotflash_amd.attention")  # the module, not the function
+    gate = impl._is_measured_t4_runtime.__wrapped__  # past its per-device cache
+    assert gate(0) is False
+    stack = {
+        "triton": ("triton_turing_supported", lambda: True),
+        "cuda": ("version.cuda", "12.4"),
+        "available": ("cuda.is_available", lambda: True),
+        "capability": ("cuda.get_device_capability", lambda d: (7, 5)),
+        "name": ("cuda.get_device_name", lambda d: "Tesla T4"),
+        "torch": ("__version__", "2.6.0+cu124"),
+    }
+    wrong = {"triton": lambda: False, "cuda": None, "available": lambda: False,
+             "capability": lambda d: (8, 0), "name": lambda d: "NVIDIA A10", "torch": "2.5.1"}
+
+    def apply(mp, key, value):
+        where, val = stack[key]
+        if where == "triton_turing_supported":
+            mp.setattr(impl, "triton_turing_supported", value)
+        elif where.startswith("cuda."):
+            mp.setattr(torch.cuda, where.split(".", 1)[1], value)
+        elif where == "version.cuda":
+            mp.setattr(torch.version, "cuda", value)
+        else:
+            mp.setattr(torch, "__version__", value)
+
+    with monkeypatch.context() as mp:
+        for key, (_, val) in stack.items():
+            apply(mp, key, val)
+        assert gate(0) is True
+    for off in stack:
+        with monkeypatch.context() as mp:
+            for key, (_, val) in stack.items():
+                apply(mp, key, wrong[key] if key == off else val)
+            assert not gate(0), off
+
+
 def test_sdpa_matches_torch_mha():
     torch.manual_seed(0)
     q = torch.randn(2, 4, 17, 32)
