@@ -84,6 +84,28 @@ __host__ __device__ inline int dkdv_nq(int kt, int nqt, bool causal) {
   const int n = nqt - dkdv_qstart(kt, causal);
   return n > 0 ? n : 0;
 }
+// Key tiles that hold any visible (query, key) pair: all of them, or under
+// the causal mask those before ceil(nqt / 2) (dkdv_nq is zero from there).
+__host__ __device__ inline int dkdv_seen_tiles(int nqt, int nkt, bool causal) {
+  // dkdv_nq(kt) = nqt - 2 kt under the causal mask: zero from ceil(nqt / 2).
+  const int m = causal ? (nqt + 1) / 2 : nkt;
+  return m < nkt ? m : nkt;
+}
+// Order of the key tiles within a KV group: position pos holds tile
+// dkdv_tile_at(pos). The seen tiles alternate from both ends (0, m - 1, 1,
+// m - 2, ...), so that under the causal mask a long tile row is followed by
+// a short one; tiles that see no query come last. With the causal triangle's
+// rows, 256 - 8 kt units at config 3, each pair then costs about two
+// workgroups, and the stream-K boundaries cut every pair once, in its long
+// tile: at most two shares per tile and two segments per workgroup.
+__host__ __device__ inline int dkdv_tile_at(int pos, int m) {
+  if (pos >= m) return pos;
+  return (pos & 1) ? m - 1 - (pos >> 1) : pos >> 1;
+}
+__host__ __device__ inline int dkdv_pos_of(int kt, int m) {
+  if (kt >= m) return kt;
+  return kt < (m + 1) / 2 ? 2 * kt : 2 * (m - 1 - kt) + 1;
+}
 // Stream-K shares: workgroup w owns units [start[w], start[w + 1]). The host
 // places the boundaries by cost rather than by unit count: every key-tile row
 // a workgroup enters (a "segment") costs about kSegmentCost units on top of
@@ -94,7 +116,8 @@ constexpr int kMaxDkdvWG = 512;
 struct DkdvSplit {
   int start[kMaxDkdvWG + 1];
 };
-// Units are ordered (KV group, key tile, query head, query tile), and the
+// Units are ordered (KV group, key tile in dkdv_tile_at order, query head,
+// query tile), and the
 // shares are laid out so that XCD x (the dispatcher sends workgroup i to XCD
 // i % 8) runs shares [x nwg / 8, (x + 1) nwg / 8): one XCD's CUs then work on
 // the same KV group(s), whose Q/dO rows they all stream, and share its L2.
@@ -629,20 +652,24 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
   };
 
   // Segments: the tile row (grp, kt) holding unit u, of which this share
-  // covers units [ua, ub) (row-relative).
+  // covers units [ua, ub) (row-relative). Rows are walked by their position
+  // in the group's tile order.
   const int64_t group_units = p.units / p.ngroups;
+  const int mseen = dkdv_seen_tiles(p.nqt, p.nkt, CAUSAL);
   int grp = (int)(u / group_units);
-  int kt = 0;
+  int pos = 0;
+  int kt = dkdv_tile_at(0, mseen);
   int64_t row_base = grp * group_units;  // first unit of tile row (grp, kt)
   auto seek = [&]() {
     for (;;) {
       const int64_t row_units = (int64_t)p.G * dkdv_nq(kt, p.nqt, CAUSAL);
       if (u < row_base + row_units) break;
       row_base += row_units;
-      if (++kt == p.nkt) {
-        kt = 0;
+      if (++pos == p.nkt) {
+        pos = 0;
         ++grp;
       }
+      kt = dkdv_tile_at(pos, mseen);
     }
   };
   // A segment's set-up loads: this wave's K and V rows as B operands (lane =
@@ -962,10 +989,6 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
 // about 15 us of dispatch.
 constexpr int kFixKeys = 16;  // keys per fixup workgroup
 constexpr int kFixSub = kBNK / kFixKeys;
-__host__ inline int dkdv_first_unseen_tile(int nqt, int nkt, bool causal) {
-  // dkdv_nq(kt) = nqt - 2 kt under the causal mask: zero from ceil(nqt / 2).
-  return causal ? std::min((nqt + 1) / 2, nkt) : nkt;
-}
 template <typename T, int DT, bool CAUSAL>
 __global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p, const DkdvSplit sp) {
   const int t = blockIdx.x / kFixSub, sub = blockIdx.x % kFixSub;
@@ -986,8 +1009,12 @@ __global__ __launch_bounds__(256) void dkdv_fixup_kernel(const BwdParams p, cons
     }
     return;
   }
+  // First unit of the tile row: the rows at earlier positions of the group's
+  // tile order come before it.
+  const int mseen = dkdv_seen_tiles(p.nqt, p.nkt, CAUSAL);
   int64_t first = (int64_t)grp * (p.units / p.ngroups);
-  for (int k = 0; k < kt; ++k) first += (int64_t)p.G * dkdv_nq(k, p.nqt, CAUSAL);
+  const int kpos = dkdv_pos_of(kt, mseen);
+  for (int q = 0; q < kpos; ++q) first += (int64_t)p.G * dkdv_nq(dkdv_tile_at(q, mseen), p.nqt, CAUSAL);
   const int64_t last = first + (int64_t)p.G * nq - 1;
   const int w0 = dkdv_owner(sp, p.nwg, first), w1 = dkdv_owner(sp, p.nwg, last);
   if (w0 == w1) return;
@@ -1065,10 +1092,12 @@ static int dkdv_split(DkdvSplit& sp, int ngroups, int G, int nqt, int nkt, bool 
     int w = 1, shared = 0;
     int64_t base = 0, cost = 0;
     cached.start[0] = 0;
-    // Tile rows in unit order: KV group outer, key tile inner.
+    const int mseen = dkdv_seen_tiles(nqt, nkt, causal);
+    // Tile rows in unit order: KV group outer, key tiles in dkdv_tile_at
+    // order inner.
     for (int g = 0; g < ngroups && w < nwg; ++g) {
-      for (int kt = 0; kt < nkt && w < nwg; ++kt) {
-        const int64_t units = (int64_t)G * dkdv_nq(kt, nqt, causal);
+      for (int pos = 0; pos < nkt && w < nwg; ++pos) {
+        const int64_t units = (int64_t)G * dkdv_nq(dkdv_tile_at(pos, mseen), nqt, causal);
         if (!units) continue;
         const int64_t row_cost = 8 * units + kSegmentCost8;
         // Boundaries whose target cost falls inside this tile row.
@@ -1139,7 +1168,7 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
     p.units = dkdv_total_units(p.ngroups, p.G, p.nqt, p.nkt, causal);
     DkdvSplit sp;
     const int shared = dkdv_split(sp, p.ngroups, p.G, p.nqt, p.nkt, causal, p.nwg);
-    const int64_t unseen = (int64_t)p.ngroups * (p.nkt - dkdv_first_unseen_tile(p.nqt, p.nkt, causal));
+    const int64_t unseen = (int64_t)p.ngroups * (p.nkt - dkdv_seen_tiles(p.nqt, p.nkt, causal));
     if (shared > 0 || unseen > 0) {
       const int64_t grid = (int64_t)p.nkt * p.ngroups * kFixSub;
       if (grid > 0x7fffffff) return set_error(KF_EINVAL, "kf_attn_bwd: problem too large for one fixup launch");
