@@ -1083,40 +1083,66 @@ static int dkdv_split(DkdvSplit& sp, int ngroups, int G, int nqt, int nkt, bool 
   thread_local int cached_shared = 0;
   const Key k{ngroups, G, nqt, nkt, causal ? 1 : 0, nwg};
   if (memcmp(&k, &last, sizeof k) != 0) {
-    int64_t total = 0, all_units = 0;
+    int64_t rows_cost = 0, all_units = 0;
     for (int kt = 0; kt < nkt; ++kt) {
       const int64_t units = (int64_t)G * dkdv_nq(kt, nqt, causal);
-      if (units) total += (int64_t)ngroups * (8 * units + kSegmentCost8);
+      if (units) rows_cost += (int64_t)ngroups * (8 * units + kSegmentCost8);
       all_units += (int64_t)ngroups * units;
     }
-    int w = 1, shared = 0;
-    int64_t base = 0, cost = 0;
-    cached.start[0] = 0;
     const int mseen = dkdv_seen_tiles(nqt, nkt, causal);
-    // Tile rows in unit order: KV group outer, key tiles in dkdv_tile_at
-    // order inner.
-    for (int g = 0; g < ngroups && w < nwg; ++g) {
-      for (int pos = 0; pos < nkt && w < nwg; ++pos) {
-        const int64_t units = (int64_t)G * dkdv_nq(dkdv_tile_at(pos, mseen), nqt, causal);
-        if (!units) continue;
-        const int64_t row_cost = 8 * units + kSegmentCost8;
-        // Boundaries whose target cost falls inside this tile row.
-        bool cut = false;
-        while (w < nwg) {
-          const int64_t target = (total * w + nwg - 1) / nwg;
-          if (target > cost + row_cost) break;
-          int64_t into = (target - cost - kSegmentCost8 + 7) / 8;
-          into = into < 0 ? 0 : (into > units ? units : into);
-          cached.start[w++] = (int)(base + into);
-          cut = cut || (into > 0 && into < units);
+    // Boundaries at equal cost over the rows in unit order (KV group outer,
+    // key tiles in dkdv_tile_at order inner). A boundary inside a tile row
+    // starts one more segment (the next share enters the row part-way); with
+    // cut_cost = kSegmentCost8 that segment start is charged to the share
+    // that makes it, and `total` must then include the cuts. Returns the
+    // number of cuts; `shared` counts the rows cut at least once.
+    auto place = [&](DkdvSplit& out, int64_t total, int64_t cut_cost, int& shared_rows) {
+      int w = 1, cuts = 0;
+      int64_t base = 0, cost = 0;
+      shared_rows = 0;
+      out.start[0] = 0;
+      for (int g = 0; g < ngroups && w < nwg; ++g) {
+        for (int pos = 0; pos < nkt && w < nwg; ++pos) {
+          const int64_t units = (int64_t)G * dkdv_nq(dkdv_tile_at(pos, mseen), nqt, causal);
+          if (!units) continue;
+          const int64_t row_cost = 8 * units + kSegmentCost8;
+          int row_cuts = 0;
+          int64_t prev = 0;  // boundaries never move backwards
+          while (w < nwg) {
+            const int64_t target = (total * w + nwg - 1) / nwg;
+            if (target > cost + row_cost + row_cuts * cut_cost) break;
+            int64_t into = (target - cost - kSegmentCost8 - row_cuts * cut_cost + 7) / 8;
+            into = into < prev ? prev : (into > units ? units : into);
+            prev = into;
+            out.start[w++] = (int)(base + into);
+            if (into > 0 && into < units) ++row_cuts;
+          }
+          shared_rows += row_cuts > 0 ? 1 : 0;
+          cuts += row_cuts;
+          cost += row_cost + row_cuts * cut_cost;
+          base += units;
         }
-        shared += cut ? 1 : 0;
-        cost += row_cost;
-        base += units;
       }
+      while (w < nwg) out.start[w++] = (int)all_units;
+      out.start[nwg] = (int)all_units;
+      return cuts;
+    };
+    // The plain placement first; then the cut-charged one, started from the
+    // plain cut count and kept when it reaches a fixed point (at config 3
+    // at once: the long tile of each pair is cut once, half a segment later).
+    int shared = 0;
+    int cuts = place(cached, rows_cost, 0, shared);
+    DkdvSplit refined;
+    for (int pass = 0; pass < 3; ++pass) {
+      int rshared = 0;
+      const int rcuts = place(refined, rows_cost + (int64_t)cuts * kSegmentCost8, kSegmentCost8, rshared);
+      if (rcuts == cuts) {
+        cached = refined;
+        shared = rshared;
+        break;
+      }
+      cuts = rcuts;
     }
-    while (w < nwg) cached.start[w++] = (int)all_units;
-    cached.start[nwg] = (int)all_units;
     cached_shared = shared;
     last = k;
   }
