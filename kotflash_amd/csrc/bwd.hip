@@ -1071,7 +1071,8 @@ static size_t delta_bytes(int64_t B, int64_t Hq, int64_t Sq) {
 // kSegmentCost8 / 8 units: on the MI355X at config 3 a sweep of the weight
 // put the shortest launch at 4.5 to 6 units, and after a segment's loads
 // came to overlap the previous segment's flush, 3 and 4 units were still
-// 1-2% slower than 5.
+// 1-2% slower than 5. With the long-short tile order and cuts charged to the
+// share that makes them, 3, 7 and 10 units were 0.4-1.2% slower than 5.
 constexpr int kSegmentCost8 = 40;
 // Returns the number of tile rows that a share boundary cuts (shared tiles).
 static int dkdv_split(DkdvSplit& sp, int ngroups, int G, int nqt, int nkt, bool causal, int nwg) {
