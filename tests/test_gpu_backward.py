@@ -155,6 +155,25 @@ def test_autograd_through_public_api(dtype):
         assert_close(g, e, **BWD_TOL[dtype], what=f"split d{n}")
 
 
+@pytest.mark.parametrize("shape", [
+    # (B, Hq, Hkv, Sq, Sk, D, causal). The dK/dV schedule walks a KV group's
+    # key tiles long and short alternately and places stream-K boundaries by
+    # cost; these cases stress it.
+    (1, 8, 1, 4096, 4096, 64, True),    # one KV group: long rows cut into many shares
+    (1, 4, 2, 1100, 1100, 64, True),    # an odd number (9) of seen key tiles
+    (2, 4, 2, 300, 1000, 64, True),     # 3 seen key tiles of 8, the rest never seen
+    (1, 2, 1, 2500, 700, 128, True),    # Sq > Sk causal
+    (2, 8, 2, 1024, 1024, 128, False),  # equal rows, shares on row boundaries
+])
+def test_backward_schedule_shapes(shape):
+    b, hq, hkv, sq, sk, d, causal = shape
+    q = seeded((b, hq, sq, d), 85, dtype=F16)
+    k = seeded((b, hkv, sk, d), 86, dtype=F16)
+    v = seeded((b, hkv, sk, d), 87, dtype=F16)
+    do = seeded((b, hq, sq, d), 88, dtype=F16)
+    _check_grads(q, k, v, do, causal, F16, f"{shape}")
+
+
 @pytest.mark.parametrize("shape", [(1, 8, 2, 64, 80, 64, True), (1, 8, 1, 80, 64, 32, True),
                                    (1, 4, 2, 2048, 2048, 32, True)])
 def test_bf16_gradients_no_worse_than_torch(shape):
