@@ -194,9 +194,16 @@ __global__ __launch_bounds__(256) void delta_kernel(const BwdParams p) {
 // KS: 16-column k-steps of the contractions over head_dim (S, dP and the row
 // deltas): DT / 16, or 5 for head dims up to 80 in a 96-wide tile, whose
 // last 16 columns are zero padding.
-template <typename T, int DT, int KS, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
-  constexpr int BM = 128;
+//
+// SPLIT (short problems, the forward's split form): the workgroup owns 32
+// query rows and its four waves split the key range, wave w taking tiles w,
+// w + 4, ... through a ring of its own (two stages up to head dim 64, one
+// above, where the next tile's V loads after the S/dP product and its K after
+// the dQ product). The four fp32 dQ are summed through LDS; P already uses
+// the global LSE, so no weights are needed. Wave 0 writes the row deltas.
+template <typename T, int DT, int KS, bool CAUSAL, bool SPLIT>
+__global__ __launch_bounds__(256, SPLIT ? 1 : 2) void dq_kernel(const BwdParams p) {
+  constexpr int BM = SPLIT ? 32 : 128;
   constexpr int BN = 64;
   constexpr int CPR = DT / 8;
   constexpr int NKS = KS;
@@ -204,10 +211,17 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
   constexpr int NDB = DT / 32;
   constexpr int TB = BN * DT * 2;       // bytes of one K (or V) tile
   constexpr int STAGE_B = 2 * TB;       // K | V
-  constexpr int NKI = BN * CPR / 256;   // 1 KB loads per wave per tile and matrix
-  static_assert(BN * CPR == 256 * NKI, "tile chunks must split into whole loads");
+  constexpr int NST = (SPLIT && DT > 64) ? 1 : 2;  // ring stages
+  // 1 KB loads per wave per tile and matrix: a quarter of the tile, or all of
+  // it in the split form.
+  constexpr int NKI = BN * CPR / (SPLIT ? 64 : 256);
+  static_assert(BN * CPR == (SPLIT ? 64 : 256) * NKI, "tile chunks must split into whole loads");
+  constexpr int RING_B = (SPLIT ? 4 : 1) * NST * STAGE_B;
+  constexpr int OSTR = DT + 1;  // split form: per-wave dQ^T rows in LDS
+  constexpr int MERGE_B = SPLIT ? 4 * 32 * OSTR * 4 : 0;
+  constexpr int SMEM_B = RING_B > MERGE_B ? RING_B : MERGE_B;
   using Tile = SwizzledTile<CPR>;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE_B / 2];
+  __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM_B / 2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = wave_index();
@@ -233,7 +247,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
   }
   const int kvh = h / p.G;
   const int q0 = qt * BM;
-  const int qrow = q0 + wave * 32 + l32;
+  const int qrow = q0 + (SPLIT ? 0 : wave * 32) + l32;
   const bool row_ok = qrow < p.Sq;
 
   const auto qr = make_rsrc(p.q + b * p.q_sb + h * p.q_sh, rows_extent(p.Sq, p.q_ss, p.D));
@@ -273,7 +287,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
         dlt += Elem<T>::to_f32((uint16_t)(of[ks][w] >> 16)) * Elem<T>::to_f32((uint16_t)(dof[ks][w] >> 16));
       }
     dlt = wave_xor32_sum(dlt);
-    if (row_ok && h32 == 0) {
+    if (row_ok && h32 == 0 && (!SPLIT || wave == 0)) {
       p.delta[rowlin] = -dlt;
       p.lse2[rowlin] = lse2;
     }
@@ -285,6 +299,9 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
 
   const int nkeys = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
   const int ntiles = cdiv(nkeys, BN);
+  // This wave's tiles: all of them, or every fourth from tile `wave`.
+  const int nl = SPLIT ? (ntiles > wave ? (ntiles - wave + 3) / 4 : 0) : ntiles;
+  auto tile_of = [&](int li) { return SPLIT ? wave + 4 * li : li; };
 
   // Per-lane load plan: for each of this wave's NKI 1 KB blocks of a tile,
   // the byte offset of this lane's 16-byte chunk within the tile's rows
@@ -293,23 +310,35 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
   uint32_t koff[NKI], voff[NKI];
 #pragma unroll
   for (int k = 0; k < NKI; ++k) {
-    const int pc = (wave * NKI + k) * 64 + lane;
+    const int pc = ((SPLIT ? 0 : wave * NKI) + k) * 64 + lane;
     const int r = pc / CPR;
     const int c = (pc % CPR) ^ Tile::key(r);
     const bool ok = c * 8 < p.D;
     koff[k] = ok ? (uint32_t)(r * p.k_ss + c * 8) * 2u : kOOB;
     voff[k] = ok ? (uint32_t)(r * p.v_ss + c * 8) * 2u : kOOB;
   }
-  const uint32_t lds0 = lds_addr(smem);
+  const uint32_t lds0 = lds_addr(smem) + (SPLIT ? (uint32_t)(wave * NST * STAGE_B) : 0u);
   auto tile_load = [&](int tile, int st) {
     const uint32_t kso = (uint32_t)(tile * BN * p.k_ss) * 2u;
     const uint32_t vso = (uint32_t)(tile * BN * p.v_ss) * 2u;
-    const uint32_t m0 = lds0 + (uint32_t)st * STAGE_B + (uint32_t)(wave * NKI) * 1024u;
+    const uint32_t m0 = lds0 + (uint32_t)st * STAGE_B + (SPLIT ? 0u : (uint32_t)(wave * NKI) * 1024u);
 #pragma unroll
     for (int k = 0; k < NKI; ++k) {
       dma16_s(kr, m0 + k * 1024u, koff[k], kso);
       dma16_s(vr, m0 + TB + k * 1024u, voff[k], vso);
     }
+  };
+  // The split form's one-stage ring loads a tile's K and V separately, each
+  // once the previous tile's reads of it are done.
+  auto tile_load_k = [&](int tile) {
+    const uint32_t kso = (uint32_t)(tile * BN * p.k_ss) * 2u;
+#pragma unroll
+    for (int k = 0; k < NKI; ++k) dma16_s(kr, lds0 + k * 1024u, koff[k], kso);
+  };
+  auto tile_load_v = [&](int tile) {
+    const uint32_t vso = (uint32_t)(tile * BN * p.v_ss) * 2u;
+#pragma unroll
+    for (int k = 0; k < NKI; ++k) dma16_s(vr, lds0 + TB + k * 1024u, voff[k], vso);
   };
   // LDS read bases (bytes, stage 0, K tile, key block 0). S^T / dP^T rows:
   // lane row l32, logical chunk 2 ks + h32. dQ^T transposed reads: the
@@ -331,18 +360,21 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
       }
   }
 
-  if (ntiles > 0) tile_load(0, 0);
+  if (nl > 0) tile_load(tile_of(0), 0);
   wait_all_memory();
-  __syncthreads();
+  if constexpr (!SPLIT) __syncthreads();
 
-  const int wq0 = q0 + wave * 32;
-  // One tile on ring stage ST (a compile-time constant, so every LDS offset
-  // below is an immediate).
-  auto tile_body = [&](int it, auto stc) {
+  const int wq0 = q0 + (SPLIT ? 0 : wave * 32);
+  // This wave's li-th tile on ring stage ST (a compile-time constant, so
+  // every LDS offset below is an immediate).
+  auto tile_body = [&](int li, auto stc) {
     constexpr int ST = decltype(stc)::value;
-    if (it + 1 < ntiles) tile_load(it + 1, ST ^ 1);
-    const int kbase = it * BN;
+    if constexpr (NST == 2) {
+      if (li + 1 < nl) tile_load(tile_of(li + 1), ST ^ 1);
+    }
+    const int kbase = tile_of(li) * BN;
     const bool need_mask = (kbase + BN > p.Sk) || (CAUSAL && kbase + BN - 1 > wq0);
+    bool v_next = false;  // one-stage ring: the next tile's V already issued
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int kb0 = kbase + 32 * kb;
@@ -396,6 +428,15 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
         __builtin_amdgcn_sched_barrier(0);
       });
       __builtin_amdgcn_s_setprio(0);
+      if constexpr (NST == 1) {
+        // Every V read of this tile fed a dP product (the last key block's):
+        // the next V can land during the dQ product and the next S.
+        if (kb == 1 && li + 1 < nl) {
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          tile_load_v(tile_of(li + 1));
+          v_next = true;
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = fmaf(s[r], p.scale_log2, -lse2);
       if (need_mask) {
@@ -420,12 +461,68 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(const BwdParams p) {
       });
       __builtin_amdgcn_s_setprio(0);
     }
+    if constexpr (NST == 1) {
+      // Every K read of this tile fed an S or dQ product (and every V read a
+      // dP product, if the second key block was skipped).
+      if (li + 1 < nl) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (!v_next) tile_load_v(tile_of(li + 1));
+        tile_load_k(tile_of(li + 1));
+      }
+    }
     KF_WAIT_VMCNT(0);  // this wave's loads of the next tile
-    __syncthreads();   // every wave's loads landed; stage ST is free again
+    // Every wave's loads landed; stage ST is free again. The split form's
+    // rings are per wave, and the wave's own wait suffices.
+    if constexpr (!SPLIT) __syncthreads();
   };
-  for (int it = 0; it < ntiles; it += 2) {
-    tile_body(it, std::integral_constant<int, 0>{});
-    if (it + 1 < ntiles) tile_body(it + 1, std::integral_constant<int, 1>{});
+  if constexpr (NST == 2) {
+    for (int li = 0; li < nl; li += 2) {
+      tile_body(li, std::integral_constant<int, 0>{});
+      if (li + 1 < nl) tile_body(li + 1, std::integral_constant<int, 1>{});
+    }
+  } else {
+    for (int li = 0; li < nl; ++li) tile_body(li, std::integral_constant<int, 0>{});
+  }
+
+  if constexpr (SPLIT) {
+    // Sum the four waves' dQ^T of the same 32 rows. The buffer overlays the
+    // other waves' rings, hence the barrier first.
+    __syncthreads();
+    float* ob = reinterpret_cast<float*>(smem);  // [wave][row][OSTR]
+    {
+      float* orow = ob + (wave * 32 + l32) * OSTR;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) orow[32 * db + 8 * (r >> 2) + 4 * h32 + (r & 3)] = dq[db][r];
+    }
+    __syncthreads();
+    // Wave w stores head-dim columns [w DT/4, (w + 1) DT/4) of the 32 rows;
+    // a lane takes row l32 and half h32 of those columns.
+    constexpr int CW = DT / 4, CH = CW / 2;
+    static_assert(CH % 4 == 0, "stores are 4 columns wide");
+    if (row_ok) {
+      uint16_t* Dq = p.dq + b * p.dq_sb + h * p.dq_sh + qrow * p.dq_ss;
+      const int c0 = wave * CW + h32 * CH;
+#pragma unroll
+      for (int j = 0; j < CH; j += 4) {
+        const int d = c0 + j;
+        if (d < p.D) {
+          float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const float* src = ob + (w * 32 + l32) * OSTR + d;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] += src[e];
+          }
+          u32x2 wv;
+          wv[0] = pack2<T>(o[0] * p.scale, o[1] * p.scale);
+          wv[1] = pack2<T>(o[2] * p.scale, o[3] * p.scale);
+          *reinterpret_cast<u32x2*>(Dq + d) = wv;
+        }
+      }
+    }
+    return;
   }
 
   if (row_ok) {
@@ -1166,12 +1263,22 @@ static int launch_bwd(BwdParams p, bool causal, int stages, hipStream_t stream) 
     if (rc) return rc;
   }
   if (stages & KF_BWD_DQ) {
-    p.nqt = cdiv(p.Sq, 128);
+    // The forward's rule for its split form: grids of 128-row tiles that
+    // leave most CUs idle take 32-row workgroups whose waves split the key
+    // range.
+    const bool split = attn_use_split(p.B, p.Hq, p.Sq, p.Sk, causal);
+    p.nqt = cdiv(p.Sq, split ? 32 : 128);
     const int64_t gq = (int64_t)p.nqt * p.B * p.Hq;
-    if (causal)
-      hipLaunchKernelGGL((dq_kernel<T, DT, KS, true>), dim3((unsigned)gq), dim3(256), 0, stream, p);
-    else
-      hipLaunchKernelGGL((dq_kernel<T, DT, KS, false>), dim3((unsigned)gq), dim3(256), 0, stream, p);
+    if (split) {
+      if (causal)
+        hipLaunchKernelGGL((dq_kernel<T, DT, KS, true, true>), dim3((unsigned)gq), dim3(256), 0, stream, p);
+      else
+        hipLaunchKernelGGL((dq_kernel<T, DT, KS, false, true>), dim3((unsigned)gq), dim3(256), 0, stream, p);
+    } else if (causal) {
+      hipLaunchKernelGGL((dq_kernel<T, DT, KS, true, false>), dim3((unsigned)gq), dim3(256), 0, stream, p);
+    } else {
+      hipLaunchKernelGGL((dq_kernel<T, DT, KS, false, false>), dim3((unsigned)gq), dim3(256), 0, stream, p);
+    }
     int rc = check_launch("kf_attn_bwd(dq)");
     if (rc) return rc;
   }

@@ -494,25 +494,10 @@ __global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? 2 : 1)) void fwd_kernel
   }
 }
 
-// The split form runs when a grid of 128-row tiles would leave most of the
-// 256 CUs idle and a tile sees more than two K/V tiles: config 1's 64
-// workgroups, for instance, become 256 with chains of at most two tiles. Its
-// grid (four times the tiles, one workgroup per CU) fits one round of the
-// CUs up to 64 tiles; causal grids, whose tiles differ in length, still gain
-// up to 128. Measured on MI355X against the tiled form: config 1 -37%;
-// 256 tiles or non-causal D >= 96 at 96-128 tiles run 5-20% slower split.
-constexpr int64_t kFwdSplitMaxTiles = 64;
-constexpr int64_t kFwdSplitMaxTilesCausal = 128;
-
-static bool fwd_use_split(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, bool causal) {
-  const int64_t tiles = (Sq + 127) / 128 * B * Hq;
-  return Sk > 128 && tiles <= (causal ? kFwdSplitMaxTilesCausal : kFwdSplitMaxTiles);
-}
-
 template <typename T, int DT, int KS, int QB>
 static int launch_fwd(const FwdParams& prm, bool causal, hipStream_t stream) {
   FwdParams p = prm;
-  const bool split = QB == 1 && fwd_use_split(p.B, p.Hq, p.Sq, p.Sk, causal);
+  const bool split = QB == 1 && attn_use_split(p.B, p.Hq, p.Sq, p.Sk, causal);
   const int BM = split ? 32 : 4 * QB * 32;
   p.nqt = cdiv(p.Sq, BM);
   const int64_t grid = (int64_t)p.nqt * p.B * p.Hq;

@@ -27,4 +27,21 @@ inline int head_tile(int64_t D) {
   return 128;
 }
 
+// The split forms of the forward and dQ kernels (32-row workgroups whose
+// waves split the key range) run when a grid of 128-row tiles would leave
+// most of the 256 CUs idle and a tile sees more than two K/V tiles: config
+// 1's 64 workgroups, for instance, become 256 with chains of at most two
+// tiles. The split grid (four times the tiles, one workgroup per CU) fits
+// one round of the CUs up to 64 tiles; causal grids, whose tiles differ in
+// length, still gain up to 128. Measured on MI355X for the forward against
+// the tiled form: config 1 -37%; 256 tiles, or non-causal D >= 96 at 96-128
+// tiles, 5-20% slower split.
+constexpr int64_t kSplitMaxTiles = 64;
+constexpr int64_t kSplitMaxTilesCausal = 128;
+
+inline bool attn_use_split(int64_t B, int64_t Hq, int64_t Sq, int64_t Sk, bool causal) {
+  const int64_t tiles = (Sq + 127) / 128 * B * Hq;
+  return Sk > 128 && tiles <= (causal ? kSplitMaxTilesCausal : kSplitMaxTiles);
+}
+
 }  // namespace kf
