@@ -174,6 +174,41 @@ def test_backward_schedule_shapes(shape):
     _check_grads(q, k, v, do, causal, F16, f"{shape}")
 
 
+@pytest.mark.parametrize("shape", [
+    # (B, Hq, Hkv, Sq, Sk, D, causal): the split dQ form with one-stage rings
+    # (D > 64) in bf16.
+    (1, 2, 1, 2500, 700, 128, True),
+    (2, 16, 4, 512, 512, 96, True),
+])
+def test_backward_split_dq_bf16(shape):
+    """dQ (the split form under test) at the bf16 bar |a - b| <= 1e-2 +
+    1e-2 |ref|. dK/dV come from the dK/dV kernel; at the second shape that bar
+    is at the edge of bf16 itself: torch's bf16 SDPA backward on the same
+    inputs misses it on 7 dK and 4 dV elements (up to 1.2x and 1.44x the
+    bound), this build on one dK element (1.009x). They are held to the
+    no-worse-than-torch criterion of test_bf16_gradients_no_worse_than_torch."""
+    b, hq, hkv, sq, sk, d, causal = shape
+    q = seeded((b, hq, sq, d), 89, dtype=BF16)
+    k = seeded((b, hkv, sk, d), 90, dtype=BF16)
+    v = seeded((b, hkv, sk, d), 91, dtype=BF16)
+    do = seeded((b, hq, sq, d), 92, dtype=BF16)
+    scale = 1 / math.sqrt(d)
+    out, lse = attention_forward(q, k, v, causal=causal, scale=scale)
+    dq, dk, dv = attention_backward(q, k, v, out, lse, do, causal=causal, scale=scale)
+    _, _, (eq, ek, ev) = reference_fp32(q, k, v, causal=causal, with_grad_out=do)
+    assert_close(dq, eq, **BWD_TOL[BF16], what=f"{shape} dQ")
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    g = hq // hkv
+    to = torch.nn.functional.scaled_dot_product_attention(
+        qq, kk.repeat_interleave(g, 1).contiguous(), vv.repeat_interleave(g, 1).contiguous(),
+        is_causal=causal)
+    _, tk, tv = torch.autograd.grad(to, (qq, kk, vv), do)
+    for a, t, e, n in ((dk, tk, ek, "k"), (dv, tv, ev, "v")):
+        ea = float((a.float() - e).abs().max())
+        et = float((t.float() - e).abs().max())
+        assert ea <= 1.25 * et + 2e-3, f"{shape} d{n}: ours {ea:.4f} vs torch {et:.4f}"
+
+
 @pytest.mark.parametrize("shape", [(1, 8, 2, 64, 80, 64, True), (1, 8, 1, 80, 64, 32, True),
                                    (1, 4, 2, 2048, 2048, 32, True)])
 def test_bf16_gradients_no_worse_than_torch(shape):
