@@ -6,9 +6,10 @@
 //   - Q rows in registers as MFMA B operands,
 //   - the running max m, the running denominator l and the output accumulator
 //     O^T (head_dim x rows) in registers.
-// The workgroup streams K/V in tiles of BN = 64 keys through LDS (register
-// prefetch of tile n+1 overlaps the MFMAs of tile n; LDS is double-buffered so
-// one barrier per tile suffices).
+// The workgroup streams K/V in tiles of BN = 64 keys through a two-stage LDS
+// ring filled by direct-to-LDS loads one tile ahead, so one barrier per tile
+// suffices. Short problems take the split form (SPLIT, below): 32 rows per
+// workgroup, the four waves splitting the key range.
 //
 // Per tile and 32-row block the wave computes S^T = K Q^T (keys x rows), so a
 // lane owns one query row and 32 of the tile's 64 scores in registers: the row
