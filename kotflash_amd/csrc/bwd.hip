@@ -10,7 +10,9 @@
 //   2. dq_kernel (query-stationary, same layout as the forward, two waves per
 //      SIMD): per key tile it recomputes S^T = K Q^T and dP^T = V dO^T, forms
 //      dS^T = P^T (dP^T - delta) with P = exp(scale S - LSE), and accumulates
-//      dQ^T += K^T dS^T; dQ = scale * dQ (reference :17-91).
+//      dQ^T += K^T dS^T; dQ = scale * dQ (reference :17-91). Short problems
+//      take a split form: 32 rows per workgroup, the waves splitting the key
+//      range, their dQ summed through LDS.
 //   3. dkdv_kernel (key-stationary, 4 waves, one per SIMD): a key tile is 128
 //      keys of one (batch, kv_head); wave w keeps keys 32 w .. +31 in
 //      registers. For every query head of the GQA group and every 64-row query
@@ -19,11 +21,12 @@
 //      query heads happens in registers (reference :94-195, group loop
 //      :136-137, products :183-184). Work is split stream-K style: the
 //      (KV group, key tile, head, query tile) units of all tiles are laid end
-//      to end and every workgroup takes an equal share, so causal tiles of
-//      very different sizes still keep every CU busy until the end; the
-//      shares of one XCD are consecutive, so its CUs stream the same KV
-//      group's Q/dO rows through one L2. A tile shared by several workgroups
-//      is written as fp32 partials and
+//      to end and every workgroup takes an equal share of the cost, so causal
+//      tiles of very different sizes still keep every CU busy until the end;
+//      a group's key tiles are walked long and short alternately, so that
+//      shares cut few tiles; the shares of one XCD are consecutive, so its
+//      CUs stream the same KV group's Q/dO rows through one L2. A tile shared
+//      by several workgroups is written as fp32 partials and
 //   4. dkdv_fixup_kernel sums those partials (and zero-fills keys that no query
 //      can see); the reference instead splits long query ranges into a fixed
 //      number of fp32 partial copies plus a reduction pass (:198-332).
