@@ -2,7 +2,8 @@
 and ragged Sq / Sk, head dims from 8 to 128 (padded and tile-tail cases),
 causal and not. The shapes fall on both sides of the split-form rule (the
 forward and dQ kernels) and give the dK/dV stream-K planner many different
-share layouts. fp16, against fp32 autograd at the standard bars."""
+share layouts. fp16 against fp32 autograd at the standard bars, and bf16
+against fp32 and PyTorch's own bf16 SDPA."""
 import math
 import random
 
@@ -48,3 +49,35 @@ def test_random_shape_forward_backward(shape):
     assert_close(dq, eq, **BWD_TOL[F16], what=f"{what} dQ")
     assert_close(dk, ek, **BWD_TOL[F16], what=f"{what} dK")
     assert_close(dv, ev, **BWD_TOL[F16], what=f"{what} dV")
+
+
+BF16 = torch.bfloat16
+
+
+@pytest.mark.parametrize("shape", _shapes(n=12, seed=4202))
+def test_random_shape_bf16(shape):
+    """bf16: O and LSE at the bf16 bar; gradients no worse than PyTorch's own
+    bf16 SDPA backward on the same inputs (x1.25 + 2e-3), the criterion of
+    test_bf16_gradients_no_worse_than_torch: at some shapes the 1e-2 bar is
+    at the edge of bf16 itself."""
+    b, hq, hkv, sq, sk, d, causal = shape
+    q = seeded((b, hq, sq, d), 511, dtype=BF16)
+    k = seeded((b, hkv, sk, d), 512, dtype=BF16)
+    v = seeded((b, hkv, sk, d), 513, dtype=BF16)
+    do = seeded((b, hq, sq, d), 514, dtype=BF16)
+    scale = 1 / math.sqrt(d)
+    out, lse = attention_forward(q, k, v, causal=causal, scale=scale)
+    ours = attention_backward(q, k, v, out, lse, do, causal=causal, scale=scale)
+    eo, el, exact = reference_fp32(q, k, v, causal=causal, with_grad_out=do)
+    assert_close(out, eo, **FWD_TOL[BF16], what=f"{shape} O")
+    assert_close(lse, el, **FWD_TOL[BF16], what=f"{shape} LSE")
+    qq, kk, vv = (t.clone().requires_grad_(True) for t in (q, k, v))
+    g = hq // hkv
+    to = torch.nn.functional.scaled_dot_product_attention(
+        qq, kk.repeat_interleave(g, 1).contiguous(), vv.repeat_interleave(g, 1).contiguous(),
+        is_causal=causal, scale=scale)
+    theirs = torch.autograd.grad(to, (qq, kk, vv), do)
+    for a, t, e, n in zip(ours, theirs, exact, "qkv"):
+        ea = float((a.float() - e).abs().max())
+        et = float((t.float() - e).abs().max())
+        assert ea <= 1.25 * et + 2e-3, f"{shape} d{n}: ours {ea:.4f} vs torch {et:.4f}"
