@@ -87,8 +87,15 @@ __device__ inline void fwd_map_block(int bid, int nqt, int B, int Hq, int Hkv, i
 // 2^(m_w - M) / sum_w l_w 2^(m_w - M), as split-KV partials are (reference
 // triton_forward.py:269-349). The longest chain of dependent tiles is a
 // quarter of the unsplit kernel's, and the grid four times as large.
+//
+// Occupancy: two workgroups per CU, or three for the 96-wide tile (48 KB of
+// LDS each, and 168 VGPRs with a 16-byte spill outside the tile loop). Three
+// took the config 4 forward (768 equal tiles, one and a half rounds at two
+// per CU) 3.5-5% faster at D = 72 and 96 and a causal D = 96 grid of 1024
+// tiles 3% faster, bit-identical; the 64- and 32-wide tiles fit three too
+// but ran within 0.2% of two, and the 128-wide tile's LDS does not fit.
 template <typename T, int DT, int KS, int QB, bool CAUSAL, bool SPLIT>
-__global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? 2 : 1)) void fwd_kernel(const FwdParams p) {
+__global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? (DT == 96 ? 3 : 2) : 1)) void fwd_kernel(const FwdParams p) {
   static_assert(!SPLIT || QB == 1, "the split form has one 32-row block per workgroup");
   constexpr int BM = SPLIT ? 32 : 4 * QB * 32;
   constexpr int BN = 64;
