@@ -26,8 +26,6 @@ One JSON line on stdout (everything else goes to stderr):
   replays of back-to-back calls over 32 rotating K/V sets (537 MB, larger than
   the 256 MB Infinity Cache), the median of 5 timed batches of replays, and
   HBM GB/s of the 16,781,376 algorithmic bytes.
-  ``decode.floor`` times probe kernels in the same setting: the decode's K/V
-  loads alone, those followed by a merge-shaped launch, and an empty launch.
 * ``configs``: the other BASELINE configurations timed on the GPU: config 1
   (forward only), config 2 over Sk in {2048, 4096, 8192, 16384}, config 3 in
   bf16, config 4 (non-causal MHA fwd+bwd, D = 72 and 96) and config 5 (64
@@ -304,131 +302,6 @@ def bench_decode(torch, _hip, dtype, sk, replays=20):
                        f"median of {REPLAY_BATCHES} batches of {replays} replays")
 
 
-def bench_decode_floor(torch, _hip, sk=16384, replays=20):
-    """The decode's floor at config 2 (Sk=16384), in the setting of
-    bench_decode (HIP-graph replays of 32 back-to-back calls over 32 K/V
-    sets): the kernels of libkotflash_probe.so (kotflash_amd/csrc/probe)
-    issue exactly the decode's K/V loads and nothing else, a merge-shaped
-    second launch, or an empty launch; the decode itself runs beside them.
-    Returns microseconds per call, or None when the probe library is not
-    built."""
-    import ctypes
-    from pathlib import Path
-
-    path = Path(__file__).resolve().parent / "kotflash_amd" / "libkotflash_probe.so"
-    if not path.is_file():
-        return None
-    lib = ctypes.CDLL(str(path))
-    P, I, I64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
-    lib.kfp_stream.argtypes = [P, P, P, I64, I64, I64, I64, I, P]
-    lib.kfp_merge_like.argtypes = [P, P, I64, I, I64, P]
-    lib.kfp_empty.argtypes = [P]
-    for f in (lib.kfp_stream, lib.kfp_merge_like, lib.kfp_empty):
-        f.restype = I
-    c = dict(CFG2, Sk=sk)
-    b, hq, hkv, sq, d = c["B"], c["Hq"], c["Hkv"], c["Sq"], c["D"]
-    nsets = 32
-    ks = [seeded(torch, (b, hkv, sk, d), 1000 + i, torch.float16) for i in range(nsets)]
-    vs = [seeded(torch, (b, hkv, sk, d), 2000 + i, torch.float16) for i in range(nsets)]
-    q = seeded(torch, (b, hq, sq, d), 3000, torch.float16)
-    out = torch.empty_like(q)
-    splits = _hip.decode_num_splits(b, hq, hkv, sq, sk, d)
-    chunk = -(-sk // splits)
-    ws = torch.empty(max(256, _hip.decode_workspace_bytes(b, hq, hkv, sq, d, splits)),
-                     device=q.device, dtype=torch.uint8)
-    sink = torch.empty(b * hkv * splits * 4, device=q.device, dtype=torch.int32)
-    rows = b * hq * sq
-    part = torch.zeros(rows * splits * d, device=q.device, dtype=torch.float32)
-    merged = torch.empty(rows * d, device=q.device, dtype=torch.float32)
-
-    def stream(i, st):
-        rc = lib.kfp_stream(ks[i].data_ptr(), vs[i].data_ptr(), sink.data_ptr(), b * hkv, sk, d,
-                            chunk, splits, st)
-        if rc:
-            raise RuntimeError("kfp_stream failed")
-
-    def merge(st):
-        if lib.kfp_merge_like(part.data_ptr(), merged.data_ptr(), rows, splits, d, st):
-            raise RuntimeError("kfp_merge_like failed")
-
-    def decode(i, st):
-        _hip.decode(q, ks[i], vs[i], out, None, None, scale=1.0 / math.sqrt(d),
-                    num_splits=splits, workspace=ws)
-
-    variants = {
-        "empty_launch": lambda st: [lib.kfp_empty(st) for _ in range(nsets)],
-        "stream": lambda st: [stream(i, st) for i in range(nsets)],
-        "stream_then_merge": lambda st: [f(st) for i in range(nsets)
-                                         for f in (lambda s2, i=i: stream(i, s2), merge)],
-        "decode": lambda st: [decode(i, st) for i in range(nsets)],
-    }
-    res = {}
-    for name, calls in variants.items():
-        stream_ = torch.cuda.Stream()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(stream_):
-            calls(stream_.cuda_stream)
-            torch.cuda.synchronize()
-            with torch.cuda.graph(graph, stream=stream_):
-                calls(stream_.cuda_stream)
-        graph.replay()
-        torch.cuda.synchronize()
-        res[name] = replay_median_us(torch, graph, replays, nsets)
-    nbytes = 2 * b * hkv * sk * d * 2 + b * hq * sq * d * 2 * 2 + b * hq * sq * 4
-    res = {f"{k}_us": v for k, v in res.items()}
-    res["stream_hbm_frac"] = nbytes / (res["stream_us"] * 1e-6) / PEAK_HBM
-    res["note"] = ("probe kernels (kotflash_amd/csrc/probe/decode_floor.hip) in the decode line's "
-                   "graph setting: the decode's K/V loads alone, then followed by a merge-shaped "
-                   "launch, and an empty launch")
-    return res
-
-
-def bench_issue_rates(torch):
-    """Shader cycles per v_mfma_f32_32x32x16_f16 when each MFMA is followed
-    by 0-8 instructions of one kind (v_fma_f32, v_exp_f32, ds_read_b128,
-    ds_read_b64_tr_b16), or by one LDS read (two transposed ones) or one
-    exponential and N v_fma_f32, one wave on every SIMD: the probe kernel of
-    kotflash_amd/csrc/probe/issue_rate.hip. Cycles are the wave's own
-    s_memtime span per MFMA; the clock is that span over s_memrealtime
-    (100 MHz). Returns None when the probe library is not built."""
-    import ctypes
-    from pathlib import Path
-
-    path = Path(__file__).resolve().parent / "kotflash_amd" / "libkotflash_probe.so"
-    if not path.is_file():
-        return None
-    lib = ctypes.CDLL(str(path))
-    lib.kfp_issue_rate.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                                   ctypes.c_void_p, ctypes.c_void_p]
-    lib.kfp_issue_rate.restype = ctypes.c_int
-    lib.kfp_issue_rounds.restype = ctypes.c_int
-    props = torch.cuda.get_device_properties(0)
-    blocks = 4 * props.multi_processor_count  # one wave per SIMD
-    sink = torch.empty(blocks * 64, device="cuda", dtype=torch.float32)
-    ticks = torch.zeros(blocks * 2, device="cuda", dtype=torch.int64)
-    st = torch.cuda.current_stream().cuda_stream
-    mfmas = 2 * lib.kfp_issue_rounds()
-    kinds = {"v_fma_f32": 0, "v_exp_f32": 1, "ds_read_b128": 2, "ds_read_b64_tr_b16": 3,
-             "ds_read_b128 + N v_fma_f32": 4, "2 ds_read_b64_tr_b16 + N v_fma_f32": 5,
-             "v_exp_f32 + N v_fma_f32": 6, "s_add_u32": 7, "s_waitcnt (satisfied)": 8,
-             "s_nop 0": 9}
-    res = {"waves_per_simd": 1, "workgroups": blocks}
-    for name, kind in kinds.items():
-        row = {}
-        for nv in (0, 2, 3, 4, 5, 6, 8):
-            for _ in range(2):  # the second launch is the one read (warm clocks)
-                if lib.kfp_issue_rate(kind, nv, blocks, sink.data_ptr(), ticks.data_ptr(), st):
-                    raise RuntimeError("kfp_issue_rate failed")
-            t = ticks.view(blocks, 2).double().mean(0).tolist()
-            row[str(nv)] = round(t[0] / mfmas, 1)
-            if name == "v_fma_f32" and nv == 0:
-                res["shader_mhz"] = round(t[0] / t[1] * 100.0)
-        res[name] = row
-    res["note"] = ("shader cycles per MFMA (32x32x16 f16, two independent accumulators) with "
-                   "N instructions of the kind after each MFMA, keyed by N")
-    return res
-
-
 def bench_config5(torch, _hip, steps=64, seed=500):
     """cache [8, 8, 32768, 64] fp16 with per-sequence
     lengths U[4096, 28000] (seeded); each of `steps` steps appends n in
@@ -484,7 +357,7 @@ def bench_config5(torch, _hip, steps=64, seed=500):
 
     def append(i):
         nk, nv, starts = plan[i][0], plan[i][1], plan[i][2]
-        _hip.kv_append(kc, vc, nk, nv, start_dev=starts)
+        _hip.kv_append(kc, vc, nk, nv, start_dev=starts, max_start=plan[i][4] - nk.shape[2])
 
     def decode(i):
         _, _, _, seqlens, maxlen, q, out, splits, ws, _ = plan[i]
@@ -711,12 +584,6 @@ def main() -> int:
     ap.add_argument("--pmc-sample", action="store_true",
                     help="run two config 3 steps plus a calibration fill/copy for rocprofv3 "
                          "--pmc and exit (prints no bench line)")
-    ap.add_argument("--decode-floor", action="store_true",
-                    help="run only the config 2 decode floor probes beside the decode (graph "
-                         "replays) for a kernel trace and exit (prints no bench line)")
-    ap.add_argument("--issue-rates", action="store_true",
-                    help="run only the MFMA issue-overlap probe (one wave per SIMD) and exit "
-                         "(prints no bench line)")
     ap.add_argument("--only-config5", action="store_true",
                     help="run only the config 5 append/decode loops (two-launch and fused) for "
                          "a kernel trace and exit (prints no bench line)")
@@ -748,12 +615,6 @@ def main() -> int:
     if args.only_config5:
         log(json.dumps(bench_config5(torch, _hip)))
         return 0
-    if args.decode_floor:
-        log(json.dumps(bench_decode_floor(torch, _hip)))
-        return 0
-    if args.issue_rates:
-        log(json.dumps(bench_issue_rates(torch)))
-        return 0
 
     ms, wall_ms, dkdv_live, per, work, step_flops, prewarm_steps = bench_train(
         torch, _hip, dtype, args.steps, args.warmup, prewarm_ms=args.prewarm_ms)
@@ -777,7 +638,6 @@ def main() -> int:
                           "6 us to a step, so the timed steps carry none)"}
     decode = None if args.no_decode else bench_decode(torch, _hip, torch.float16, CFG2["Sk"])
     if decode:
-        decode["floor"] = bench_decode_floor(torch, _hip)
         log(f"decode: {decode}")
     side = None if args.no_side else side_configs(torch, _hip, max(20, args.steps // 4))
     if side:

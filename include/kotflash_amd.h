@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define KF_ABI_VERSION 5
+#define KF_ABI_VERSION 6
 
 enum kf_status {
   KF_OK = 0,
@@ -198,9 +198,12 @@ int kf_attn_decode_noalloc(const void* q, const void* k, const void* v, void* o,
 /*
  * K/V cache append: cache[b, h, start_b + t, :] = new[b, h, t, :] for K and V
  * in one launch, bit-exact. start_b = start_dev[b] when start_dev (device
- * int64 [B]) is non-null, else the scalar start. Rows that would land at or
- * beyond `capacity` are not written (callers validate first; the reference
- * rejects such appends before launching). new_k/new_v may have any strides
+ * int64 [B]) is non-null, else the scalar start. With start_dev, `start` is
+ * the host-side bound max_b start_dev[b]. Either way the call is rejected with
+ * KF_EINVAL before any launch unless 0 <= start and start + Snew <= capacity,
+ * as the reference rejects an out-of-range append (kv_append_cuda.cu:72-73);
+ * a device start outside [0, start] breaks the caller's bound and its rows
+ * are not written. new_k/new_v may have any strides
  * (int64_t[4], element units, including head_dim); the caches need a unit
  * head_dim stride.
  * Replaces append_kv_cuda / append_kv_ (reference
@@ -225,9 +228,12 @@ int kf_kv_append(void* k_cache, void* v_cache, const void* new_k, const void* ne
  * (num_splits from kf_decode_num_splits / _ragged over those lengths; 0 keys
  * allowed); one more split reads the new tokens from their own buffer and a
  * single workgroup per (b, kv_head) writes them into the cache (bit-exact).
- * Workspace: kf_decode_workspace_bytes(..., num_splits + 1). Positions at or
- * beyond `capacity` are not written (callers validate first, as the
- * reference does). Caches, q, new_k/new_v and o need a unit head_dim stride.
+ * Workspace: kf_decode_workspace_bytes(..., num_splits + 1). The call is
+ * rejected with KF_EINVAL before any launch unless max_length + Snew <=
+ * capacity (the reference's capacity check, kv_append_cuda.cu:72-73, applied
+ * to the host-side bound); a device length outside [0, max_length] breaks
+ * that bound: it attends to max_length keys and its new tokens are not
+ * written. Caches, q, new_k/new_v and o need a unit head_dim stride.
  * Replaces attention_forward_strided_append + _strided_decode_append_split
  * (reference kotflash/kernels/triton_decode.py:302-386, :108-238), which
  * folds one token's slot write into its split kernel; here Snew >= 1 tokens

@@ -19,7 +19,7 @@ from typing import Optional
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libkotflash_amd.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 KF_F16, KF_BF16 = 0, 1
 KF_BWD_DELTA, KF_BWD_DQ, KF_BWD_DKDV, KF_BWD_DKDV_FIXUP = 1, 2, 4, 8
 KF_BWD_ALL = KF_BWD_DELTA | KF_BWD_DQ | KF_BWD_DKDV | KF_BWD_DKDV_FIXUP
@@ -324,8 +324,16 @@ def decode_noalloc(q, k, v, out, lse: Optional[torch.Tensor], seqlens: Optional[
 
 
 def kv_append(k_cache, v_cache, new_k, new_v, *, start: int = 0,
-              start_dev: Optional[torch.Tensor] = None) -> None:
+              start_dev: Optional[torch.Tensor] = None, max_start: Optional[int] = None) -> None:
+    """kf_kv_append at the scalar ``start``, or at the per-sequence device
+    positions ``start_dev`` (int64 [B]) whose host-side maximum is
+    ``max_start``; the library rejects the call before launching unless the
+    range ends inside the capacity."""
     b, h, s, d = new_k.shape
+    if start_dev is not None:
+        if max_start is None:
+            raise ValueError("kv_append with start_dev needs max_start, the host-side bound")
+        start = max_start
     keep = [_strides(t) for t in (k_cache, v_cache, new_k, new_v)]
     with _DeviceGuard(k_cache.device):
         rc = lib().kf_kv_append(

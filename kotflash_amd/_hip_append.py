@@ -66,7 +66,7 @@ def append_kv_hip(k_cache, v_cache, new_k, new_v, start: Union[int, torch.Tensor
         for s in starts:
             if s < 0 or s + n > capacity:
                 raise RuntimeError("append range exceeds cache capacity")
-        _hip.kv_append(k_cache, v_cache, new_k, new_v, start_dev=start)
+        _hip.kv_append(k_cache, v_cache, new_k, new_v, start_dev=start, max_start=max(starts))
     else:
         start = int(start)
         if start < 0 or start + new_k.shape[2] > k_cache.shape[2]:

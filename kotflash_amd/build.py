@@ -64,26 +64,6 @@ def _compile(src: Path, verbose: bool) -> Path:
     return obj
 
 
-PROBE_DIR = CSRC / "probe"
-PROBE_LIB_PATH = PKG_DIR / "libkotflash_probe.so"
-
-
-def build_probes(verbose: bool = False) -> Path:
-    """Compile the measurement probes (``csrc/probe``, used by
-    ``bench.py --decode-floor``) into ``libkotflash_probe.so``, a library of
-    their own: they are not part of the attention C ABI."""
-    srcs = sorted(PROBE_DIR.glob("*.hip"))
-    tmp = PROBE_LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIP_FLAGS, "-shared", "-o", str(tmp), *map(str, srcs)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError("probe build failed:\n" + res.stdout + res.stderr)
-    os.replace(tmp, PROBE_LIB_PATH)
-    return PROBE_LIB_PATH
-
-
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
     """Compile every source and link ``libkotflash_amd.so``; returns its path."""
     BUILD_DIR.mkdir(exist_ok=True)
@@ -101,7 +81,6 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     if res.returncode != 0:
         raise RuntimeError("link failed:\n" + res.stdout + res.stderr)
     os.replace(tmp, LIB_PATH)
-    build_probes(verbose)
     return LIB_PATH
 
 

@@ -7,8 +7,11 @@
 //    caches append every sequence at its own position in one launch;
 //  * when every row is 16-byte aligned each thread moves 16 bytes (8 elements)
 //    of K and of V; otherwise one element per thread, like the reference;
-//  * rows whose destination position would fall outside [0, capacity) are
-//    skipped instead of written (the host validates before launching).
+//  * with per-sequence starts the host passes their maximum as a bound and the
+//    launch is rejected unless bound + S fits the capacity (the reference's
+//    capacity check, kv_append_cuda.cu:72-73, applied to that bound); a
+//    device start outside [0, bound] breaks the caller's contract: its rows
+//    are not written, so nothing lands outside [0, capacity).
 #include "kf_common.hpp"
 #include "kf_host.hpp"
 
@@ -26,7 +29,6 @@ struct AppendParams {
   int64_t nk_sb, nk_sh, nk_ss, nk_sd;
   int64_t nv_sb, nv_sh, nv_ss, nv_sd;
   int64_t total;  // work items
-  int64_t capacity;
   int B, H, S, D;
 };
 
@@ -41,8 +43,10 @@ __global__ __launch_bounds__(256) void append_kernel(const AppendParams p) {
   rest /= p.S;
   const int h = (int)(rest % p.H);
   const int b = (int)(rest / p.H);
-  const int64_t pos = (p.start_dev ? p.start_dev[b] : p.start) + t;
-  if (pos < 0 || pos >= p.capacity) return;
+  const int64_t s0 = p.start_dev ? p.start_dev[b] : p.start;
+  // With start_dev, p.start is the host's bound on it (checked to fit).
+  if (s0 < 0 || s0 > p.start) return;
+  const int64_t pos = s0 + t;
   if (VEC) {
     const int d = c * 8;
     const u32x4 kk = ldg16(p.nk + b * p.nk_sb + h * p.nk_sh + t * p.nk_ss + d);
@@ -77,8 +81,12 @@ extern "C" int kf_kv_append(void* k_cache, void* v_cache, const void* new_k, con
     return set_error(KF_EINVAL, "%s: new K/V dimensions must be non-empty", what);
   if (dtype != KF_F16 && dtype != KF_BF16)
     return set_error(KF_EINVAL, "%s: dtype must be KF_F16 or KF_BF16", what);
-  if (start_dev == nullptr && (start < 0 || start + Snew > capacity))
-    return set_error(KF_EINVAL, "%s: append range exceeds cache capacity", what);
+  // The scalar start, or with start_dev the host-side bound on every
+  // start_dev[b]: either way the whole range must fit before anything launches.
+  if (start < 0 || start + Snew > capacity)
+    return set_error(KF_EINVAL, "%s: append range exceeds cache capacity (%s %lld + %lld new "
+                     "tokens > capacity %lld)", what, start_dev ? "max start" : "start",
+                     (long long)start, (long long)Snew, (long long)capacity);
   if (B > 0x7fffffff || H > 0x7fffffff || Snew > 0x7fffffff || D > 0x7fffffff)
     return set_error(KF_EUNSUPPORTED, "%s: dimension too large", what);
   AppendParams p{};
@@ -89,7 +97,6 @@ extern "C" int kf_kv_append(void* k_cache, void* v_cache, const void* new_k, con
   p.vc_sb = v_cache_strides[0]; p.vc_sh = v_cache_strides[1]; p.vc_ss = v_cache_strides[2];
   p.nk_sb = new_k_strides4[0]; p.nk_sh = new_k_strides4[1]; p.nk_ss = new_k_strides4[2]; p.nk_sd = new_k_strides4[3];
   p.nv_sb = new_v_strides4[0]; p.nv_sh = new_v_strides4[1]; p.nv_ss = new_v_strides4[2]; p.nv_sd = new_v_strides4[3];
-  p.capacity = capacity;
   p.B = (int)B; p.H = (int)H; p.S = (int)Snew; p.D = (int)D;
   bool vec = D % 8 == 0 && p.nk_sd == 1 && p.nv_sd == 1 && aligned16(k_cache) && aligned16(v_cache) &&
              aligned16(new_k) && aligned16(new_v);

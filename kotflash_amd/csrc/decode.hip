@@ -55,13 +55,13 @@ struct DecParams {
   float* part_o;    // [ngroups][nsplit][RB][D]
   float* part_lse;  // [ngroups][nsplit][RB]
   const int32_t* seqlens;
-  // Fused append (decode_kernel<..., true>): the new tokens [B][Hkv][nnew][D]
-  // and the cache capacity; k/v above are then the caches themselves.
+  // Fused append (decode_kernel<..., true>): the new tokens [B][Hkv][nnew][D];
+  // k/v above are then the caches themselves.
   const uint16_t* nk;
   const uint16_t* nv;
   int64_t nk_sb, nk_sh, nk_ss;
   int64_t nv_sb, nv_sh, nv_ss;
-  int nnew, capacity;
+  int nnew;
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;
@@ -403,15 +403,16 @@ __global__ __launch_bounds__(256, 2) void decode_kernel(const DecParams p) {
     // The single owner of the append: the new split of row block 0 stores
     // new[b, kvh, t, :] to cache position seqlens[b] + t (t < nnew) in
     // 16-byte vectors, after its own loads of the new tokens (bit-exact copy).
-    // Positions at or beyond the capacity are not written (callers check).
+    // The host checked max_length + nnew <= capacity; a device length outside
+    // [0, max_length] breaks that promise and its tokens are not written.
     if (fresh && rb == 0) {
-      const int start = p.seqlens ? max(p.seqlens[b], 0) : p.Sk;
+      const int start = p.seqlens ? p.seqlens[b] : p.Sk;
+      if (start < 0 || start > p.Sk) return;
       const int cpr = p.D / 8;
       uint16_t* kc = const_cast<uint16_t*>(p.k) + b * p.k_sb + kvh * p.k_sh;
       uint16_t* vc = const_cast<uint16_t*>(p.v) + b * p.v_sb + kvh * p.v_sh;
       for (int e = tid; e < p.nnew * cpr; e += 256) {
         const int t = e / cpr, d = (e % cpr) * 8;
-        if (start + t >= p.capacity) continue;
         const uint4 kv4 = *reinterpret_cast<const uint4*>(kbase + t * kss + d);
         const uint4 vv4 = *reinterpret_cast<const uint4*>(vbase + t * vss + d);
         *reinterpret_cast<uint4*>(kc + (int64_t)(start + t) * p.k_ss + d) = kv4;
@@ -857,6 +858,12 @@ extern "C" int kf_attn_append_decode(const void* q, void* k_cache, void* v_cache
   if (Snew <= 0 || Snew > 0x3fffffff) return set_error(KF_EINVAL, "%s: Snew must be positive", what);
   if (max_length < 0 || capacity <= 0 || capacity > 0x3fffffff || max_length > capacity)
     return set_error(KF_EINVAL, "%s: need 0 <= max_length <= capacity", what);
+  // max_length bounds every lengths[b] (the host's promise), so the append
+  // range of every sequence fits iff this does (kv_append_cuda.cu:72-73).
+  if (max_length + Snew > capacity)
+    return set_error(KF_EINVAL, "%s: append range exceeds cache capacity (max_length %lld + %lld "
+                     "new tokens > capacity %lld)", what, (long long)max_length, (long long)Snew,
+                     (long long)capacity);
   if (lengths == nullptr && (past_length != max_length || past_length + Snew > capacity))
     return set_error(KF_EINVAL, "%s: past_length %lld + %lld new tokens must fit capacity %lld "
                      "(and equal max_length without per-sequence lengths)", what,
@@ -902,7 +909,6 @@ extern "C" int kf_attn_append_decode(const void* q, void* k_cache, void* v_cache
   p.nsplit = num_splits + 1;
   p.chunk = (int)chunk;
   p.nnew = (int)Snew;
-  p.capacity = (int)capacity;
   p.scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   return dtype == KF_F16 ? dispatch_decode<_Float16, true>(p, s) : dispatch_decode<__bf16, true>(p, s);

@@ -12,10 +12,15 @@ import torch
 
 from .. import _hip
 from ._layout import padded_head_dim, prepare, require_hip_tensors, unpad
-from .hip_forward import _check_shapes
+from .hip_forward import _check_shapes, check_tuning_kwargs
 
 
-def attention_backward(q, k, v, out, lse, grad_out, *, causal: bool, scale: float):
+def attention_backward(q, k, v, out, lse, grad_out, *, causal: bool, scale: float,
+                       block_m: int = 32, block_n: int = 64, num_warps: int = 4,
+                       num_stages: int = 1):
+    """Run the HIP backward; returns ``(dq, dk, dv)``. The tuning keywords are
+    the reference's (checked, otherwise unused)."""
+    check_tuning_kwargs(block_m, block_n, num_warps, num_stages)
     require_hip_tensors("HIP attention backward", q, k, v, out, grad_out)
     _check_shapes(q, k, v)
     if out.shape != q.shape or grad_out.shape != q.shape:

@@ -44,8 +44,23 @@ def _check_shapes(q, k, v) -> None:
         raise ValueError("HIP backend supports 8 <= head_dim <= 128")
 
 
-def attention_forward(q, k, v, *, causal: bool, scale: float):
-    """Run the HIP forward; returns ``(out, lse)``."""
+def check_tuning_kwargs(block_m: int, block_n: int, num_warps: int, num_stages: int) -> None:
+    """The reference launchers' tile-tuning keywords (triton_forward.py:
+    372-376, triton_backward.py:335-339) are accepted so that drop-in callers
+    such as its tile tuner keep working, and validated with the reference's
+    messages (triton_forward.py:392-395). They select nothing here: the gfx950
+    kernels' tiles are fixed per head dim by the MFMA, LDS and register plans."""
+    if block_m <= 0 or block_n <= 0:
+        raise ValueError("block_m and block_n must be positive")
+    if num_warps <= 0 or num_stages <= 0:
+        raise ValueError("num_warps and num_stages must be positive")
+
+
+def attention_forward(q, k, v, *, causal: bool, scale: float, block_m: int = 64,
+                      block_n: int = 32, num_warps: int = 4, num_stages: int = 2):
+    """Run the HIP forward; returns ``(out, lse)``. The tuning keywords are
+    the reference's (checked, otherwise unused)."""
+    check_tuning_kwargs(block_m, block_n, num_warps, num_stages)
     require_hip_tensors("HIP attention forward", q, k, v)
     _check_shapes(q, k, v)
     return forward_validated(q, k, v, causal=causal, scale=scale)

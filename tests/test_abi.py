@@ -112,6 +112,24 @@ def test_append_argument_validation():
     assert rc == 1 and "null" in lib.kf_last_error().decode()
 
 
+@pytest.mark.parametrize("bound,snew", [
+    (62, 3),    # the last token would land one past the end (kv_append_cuda.cu:72-73)
+    (64, 1),
+    (-1, 1),
+])
+def test_append_device_starts_are_bounded_on_the_host(bound, snew):
+    """With per-sequence device starts, `start` is the host-side bound on
+    them and an append that would not fit is rejected before anything is
+    launched (the start array, a fake address here, is never read)."""
+    lib = _hip.lib()
+    s3 = _arr(64 * 8, 64 * 8, 8)
+    s4 = _arr(2 * 8, 8, 8, 1)
+    rc = lib.kf_kv_append(0x1000, 0x2000, 0x3000, 0x4000, 0x5000, bound, 1, 1, snew, 8, 64,
+                          s3, s3, s4, s4, 0, None)
+    msg = lib.kf_last_error().decode()
+    assert rc == 1 and "capacity" in msg and "max start" in msg
+
+
 def test_ragged_decode_planner():
     """The ragged planner's count partitions max(lengths) into whole 128-key
     granules, sizes the chunk from the total visible keys (about 384
@@ -151,6 +169,10 @@ def _append_decode(lib, **kw):
 
 @pytest.mark.parametrize("kwargs,match", [
     (dict(past=128, max_length=128), "capacity"),          # no room for the new token
+    # Device lengths: max_length is the host-side bound on them and must leave
+    # room for every new token (kv_append_cuda.cu:72-73).
+    (dict(lengths=0x8000, max_length=120, Snew=9), "exceeds cache capacity"),
+    (dict(lengths=0x8000, max_length=128, Snew=1), "exceeds cache capacity"),
     (dict(past=99), "past_length"),                        # scalar position != max_length
     (dict(max_length=129), "max_length <= capacity"),
     (dict(Snew=0), "Snew"),

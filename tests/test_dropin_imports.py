@@ -89,3 +89,39 @@ def test_monkeypatching_through_the_reference_name_reaches_the_implementation(mo
     q = torch.randn(1, 2, 4, 8)
     kotflash.attention(q, q, q, backend="sdpa")
     assert calls == [1]
+
+
+def test_launchers_accept_the_reference_tuning_keywords():
+    """attention_forward / attention_backward take the reference launchers'
+    tuning keywords (triton_forward.py:372-376, triton_backward.py:335-339),
+    as its tile tuner passes them (benchmarks/tune_triton_tiles.py:186-190);
+    bad values get the reference's messages (triton_forward.py:392-395). On
+    CPU tensors the call then stops at the device check, after the keywords
+    were accepted."""
+    import inspect
+
+    import pytest
+    import torch
+    from kotflash.kernels.triton_backward import attention_backward
+    from kotflash.kernels.triton_forward import attention_forward
+
+    fwd = inspect.signature(attention_forward).parameters
+    bwd = inspect.signature(attention_backward).parameters
+    for params, defaults in ((fwd, (64, 32, 4, 2)), (bwd, (32, 64, 4, 1))):
+        for name, default in zip(("block_m", "block_n", "num_warps", "num_stages"), defaults):
+            assert params[name].kind is inspect.Parameter.KEYWORD_ONLY
+            assert params[name].default == default
+    q = torch.zeros(1, 2, 16, 64, dtype=torch.float16)
+    k = torch.zeros(1, 1, 16, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="block_m and block_n must be positive"):
+        attention_forward(q, k, k, causal=True, scale=0.125, block_m=0)
+    with pytest.raises(ValueError, match="num_warps and num_stages must be positive"):
+        attention_forward(q, k, k, causal=True, scale=0.125, num_stages=0)
+    with pytest.raises(ValueError, match="block_m and block_n must be positive"):
+        attention_backward(q, k, k, q, q[..., 0].float(), q, causal=True, scale=0.125, block_n=-1)
+    with pytest.raises((RuntimeError, ValueError), match="GPU|gfx950|HIP|device|CUDA"):
+        attention_forward(q, k, k, causal=True, scale=0.125, block_m=32, block_n=64,
+                          num_warps=8, num_stages=1)
+    with pytest.raises((RuntimeError, ValueError), match="GPU|gfx950|HIP|device|CUDA"):
+        attention_backward(q, k, k, q, q[..., 0].float(), q, causal=True, scale=0.125,
+                           block_m=64, block_n=128, num_warps=8, num_stages=2)

@@ -136,6 +136,48 @@ def test_device_start_out_of_range_raises_before_writing():
                       host_starts=[0, 0])
 
 
+def test_c_abi_rejects_out_of_range_device_positions():
+    """Through the C ABI alone (no Python-side range check): kf_kv_append with
+    device starts and kf_attn_append_decode with device lengths take a
+    host-side bound on those positions and reject, before any launch, a call
+    whose range would leave the capacity (kv_append_cuda.cu:72-73); the caches
+    stay unchanged. A device position beyond the bound it was given breaks the
+    caller's promise: its rows are skipped, never written out of range."""
+    from kotflash_amd import _hip
+
+    b, hkv, hq, cap, d, n = 2, 2, 8, 256, 64, 4
+    kc = torch.full((b, hkv, cap, d), float("nan"), device="cuda", dtype=F16)
+    vc = torch.full_like(kc, float("nan"))
+    kc[:, :, :200] = 0
+    vc[:, :, :200] = 0
+    k0, v0 = kc.clone(), vc.clone()
+    nk = seeded((b, hkv, n, d), 341, dtype=F16)
+    nv = seeded((b, hkv, n, d), 342, dtype=F16)
+    q = seeded((b, hq, 1, d), 343, dtype=F16)
+    starts = torch.tensor([100, 253], device="cuda")
+    with pytest.raises(RuntimeError, match="exceeds cache capacity"):
+        _hip.kv_append(kc, vc, nk, nv, start_dev=starts, max_start=253)
+    lengths = torch.tensor([100, 253], device="cuda", dtype=torch.int32)
+    out = torch.empty_like(q)
+    splits = _hip.decode_num_splits(b, hq, hkv, 1, 253, d)
+    ws = torch.empty(_hip.decode_workspace_bytes(b, hq, hkv, 1, d, splits + 1), device="cuda",
+                     dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="exceeds cache capacity"):
+        _hip.append_decode(q, kc, vc, nk, nv, out, None, lengths, past_length=0, max_length=253,
+                           scale=0.125, num_splits=splits, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(kc.view(torch.int16), k0.view(torch.int16))
+    assert torch.equal(vc.view(torch.int16), v0.view(torch.int16))
+    # A bound that fits, with one device start (150) above it (120): that
+    # sequence is skipped, the other written.
+    starts = torch.tensor([100, 150], device="cuda")
+    _hip.kv_append(kc, vc, nk, nv, start_dev=starts, max_start=120)
+    torch.cuda.synchronize()
+    assert torch.equal(kc[0, :, 100:104], nk[0]) and torch.equal(vc[0, :, 100:104], nv[0])
+    assert torch.equal(kc[1].view(torch.int16), k0[1].view(torch.int16))
+    assert torch.equal(vc[1].view(torch.int16), v0[1].view(torch.int16))
+
+
 def test_expanded_start_and_strided_seqlens_are_read_as_values():
     """Index tensors that are views (a stride-0 expand, a strided slice) are
     read by value, not as raw memory."""

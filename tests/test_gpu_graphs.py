@@ -92,7 +92,7 @@ def test_ragged_append_and_decode_graph_replays():
                      dtype=torch.uint8, device="cuda")
 
     def step():
-        _hip.kv_append(kc, vc, nk, nv, start_dev=starts)
+        _hip.kv_append(kc, vc, nk, nv, start_dev=starts, max_start=max(lengths))
         _hip.decode(q, kc[:, :, :maxlen], vc[:, :, :maxlen], out, None, seqlens, scale=0.125,
                     num_splits=splits, workspace=ws)
 
