@@ -76,3 +76,48 @@ def error_stats(actual, expected, *, atol, rtol):
     return {"max_abs": float(err.max()), "max_rel": float(rel),
             "outside": int((err > atol + rtol * e.abs()).sum()), "numel": a.numel(),
             "max_ref": float(e.abs().max())}
+
+
+def reference_algorithm_rounded(q, k, v, do, *, causal, scale=None):
+    """The reference kernels' own arithmetic, dense in fp32 on the GPU, for
+    inputs in fp16 or bf16: forward P rounded to the input dtype before the PV
+    product with the denominator summed over the unrounded P (reference
+    kotflash/kernels/triton_forward.py:128-135), O stored in the input dtype
+    (:139-158); backward delta from that stored O (triton_backward.py:45),
+    P = exp(scale S - LSE) and dS = P (dP - delta) in fp32, dS rounded before
+    the dQ and dK products and P before the dV product (:85, :183-184), dK/dV
+    summed over the query heads of a group (:136-137), every output stored in
+    the input dtype. Returns (O, dQ, dK, dV) as fp32 tensors of the stored
+    values: what the reference computes at this dtype, to set beside the exact
+    fp32 gradients (the reference itself runs fp16 only; in bf16 this is its
+    algorithm at bf16 precision)."""
+    dt = q.dtype
+    rnd = lambda t: t.to(dt).float()
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    group = q.shape[1] // k.shape[1]
+    qf, kf, vf, dof = (t.detach().float() for t in (q, k, v, do))
+    ke = kf.repeat_interleave(group, dim=1)
+    ve = vf.repeat_interleave(group, dim=1)
+    s = torch.matmul(qf, ke.transpose(-2, -1).contiguous()) * scale
+    if causal:
+        i = torch.arange(q.shape[2], device=q.device)[:, None]
+        j = torch.arange(k.shape[2], device=q.device)[None, :]
+        s = s.masked_fill(j > i, float("-inf"))
+    m = s.amax(dim=-1, keepdim=True).clamp_min(-3.0e38)
+    e = torch.exp(s - m)
+    lse = torch.log(e.sum(-1, keepdim=True)) + m
+    out = rnd(torch.matmul(rnd(e), ve) / e.sum(-1, keepdim=True))
+    del e
+    p = torch.exp(s - lse)
+    del s
+    delta = (out * dof).sum(-1, keepdim=True)
+    dp = torch.matmul(dof, ve.transpose(-2, -1).contiguous())
+    ds = p * (dp - delta)
+    del dp
+    dq = rnd(torch.matmul(rnd(ds), ke) * scale)
+    b, hq, sk, d = ke.shape
+    dk = torch.matmul(rnd(ds).transpose(-2, -1).contiguous(), qf) * scale
+    dv = torch.matmul(rnd(p).transpose(-2, -1).contiguous(), dof)
+    dk = rnd(dk.view(b, hq // group, group, sk, d).sum(2))
+    dv = rnd(dv.view(b, hq // group, group, sk, d).sum(2))
+    return out, dq, dk, dv
