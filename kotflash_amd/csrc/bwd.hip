@@ -1031,8 +1031,14 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
         }
       });
     }
-    // Every wave is done with the ring's stages: the next segment's loads
-    // can go out now, ahead of this segment's flush.
+    // Every wave is done reading the ring's stages: the next segment's loads
+    // can go out now, ahead of this segment's flush. This wave may still have
+    // the zero-filling loads of the two units past the segment's end in
+    // flight (they target its own rows of the ring, as the next segment's
+    // first loads do). That is safe without a wait because one wave's
+    // direct-to-LDS loads return, and write LDS, in issue order (the vmcnt
+    // counter decrements in order), so the older zero fills land before the
+    // next segment's data; the next segment's first vmcnt wait covers both.
     __syncthreads();
     const bool more = u + (ub - ua) < uend;
     if (more) {

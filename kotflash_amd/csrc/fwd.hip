@@ -102,7 +102,13 @@ __global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? (DT == 96 ? 3 : 2) : 1)
   constexpr int CPR = DT / 8;           // 16-byte chunks per row
   constexpr int NKS = KS;               // MFMA k-steps over head_dim
   static_assert(KS * 16 <= DT && KS * 16 > DT - 32, "KS covers the tile's head_dim");
-  constexpr int NDB = DT / 32;          // 32-wide head_dim blocks of O^T
+  // Head dims up to 80 in the 96-wide tile (TAIL): O^T columns 0-63 in two
+  // 32-wide blocks and 64-79 as a 16-wide tail of v_mfma_f32_16x16x32
+  // products, so the PV product runs 80 columns instead of 96 (the S product
+  // already stops at 80 through KS). The tiled form only; the split form
+  // keeps three 32-wide blocks.
+  constexpr bool TAIL = DT == 96 && KS == 5 && !SPLIT;
+  constexpr int NDB = TAIL ? 2 : DT / 32;  // 32-wide head_dim blocks of O^T
   constexpr int TB = BN * DT * 2;       // bytes of one K (or V) tile
   constexpr int STAGE_B = 2 * TB;       // K | V
   // Ring stages: two, shared by the workgroup; in the split form one ring per
@@ -158,6 +164,10 @@ __global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? (DT == 96 ? 3 : 2) : 1)
   }
 
   f32x16 oacc[QB][NDB];
+  // TAIL: O^T head dims 64-79 for query rows 16 hf .. 16 hf + 15 of the
+  // block; lane l, register r holds head dim 64 + 4 (l / 16) + r of row
+  // 16 hf + l % 16 (the 16x16x32 result layout).
+  f32x4 otail[QB][2];
   float m_i[QB], l_i[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
@@ -165,6 +175,7 @@ __global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? (DT == 96 ? 3 : 2) : 1)
     l_i[qb] = 0.f;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) oacc[qb][db] = zero16();
+    otail[qb][0] = otail[qb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
   const int nkeys = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
@@ -218,7 +229,7 @@ __global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? (DT == 96 ? 3 : 2) : 1)
   // 4 h + p / 4 (+ 8) of a 16-key step at head-dim block db. Other stages,
   // key blocks and key steps are whole multiples of 16 rows away, which keep
   // the swizzle key, so they are immediate offsets.
-  uint32_t rd[NKS], trv[NDB][2];
+  uint32_t rd[NKS], trv[NDB][2], trt = 0;
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) rd[ks] = lds0 + (uint32_t)Tile::chunk(l32, 2 * ks + h32) * 16u;
   {
@@ -231,6 +242,17 @@ __global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? (DT == 96 ? 3 : 2) : 1)
         const int col = 32 * db + 16 * g + 4 * (pl & 3);
         trv[db][hi] = lds0 + TB + (uint32_t)Tile::elem(r, col) * 2u;
       }
+    // TAIL: the A operand V^T[64 + i][keys] of a 32-key block for lane
+    // (i = l % 16, g4 = l / 16). Its k slots t are the keys the B operand
+    // (P^T after the lane swaps below) holds there: keys c4 + t (t < 4) and
+    // c4 + 16 + t - 4 (t >= 4) of the block, with c4 = 8 (g4 & 1) + 4 (g4 >> 1).
+    // Two transposed reads, the second 16 rows on (an immediate offset).
+    // Pairing rows c4 and c4 + 8 in one 32-lane pass keeps it conflict-free.
+    if constexpr (TAIL) {
+      const int g4 = lane >> 4;
+      const int r = 8 * (g4 & 1) + 4 * (g4 >> 1) + (pl >> 2);
+      trt = lds0 + TB + (uint32_t)Tile::elem(r, 64 + 4 * (pl & 3)) * 2u;
+    }
   }
 
   if (nl > 0) tile_load(tile_of(0), 0);
@@ -257,7 +279,10 @@ __global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? (DT == 96 ? 3 : 2) : 1)
       // of the PV product. Fences pin the order: without them the reads are
       // issued one slot ahead and every MFMA waits for its operand.
       constexpr int NS = 2 * NKS;   // S slots
-      constexpr int NPV = 4 * NDB;  // PV slots (db = j / 4, key step st = j % 4)
+      // PV slots: db = j / 4, key step st = j % 4 for j < 4 NDB; then, with
+      // TAIL, four 16x16x32 slots (key block kb = u / 2, row half hf = u % 2
+      // for u = j - 4 NDB).
+      constexpr int NPV = 4 * NDB + (TAIL ? 4 : 0);
       // Operand read-ahead in slots. For the 128-wide tile (16 S slots) 8 is
       // the measured optimum at config 3 (A/B in one process, fp16 -3.2%,
       // bf16 -3.4% against 4; 5, 6, 10 and 12 are slower and 16 spills);
@@ -269,10 +294,18 @@ __global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? (DT == 96 ? 3 : 2) : 1)
         kop[m] = *(const KF_LDS u32x4*)(uintptr_t)(rd[m % NKS] + off);
       };
       auto read_v = [&](int j) {
-        const uint32_t off = ST * STAGE_B + 16 * (j % 4) * CPR * 16;
-        const u32x2 lo = lds_read_tr16_at(trv[j / 4][0] + off);
-        const u32x2 hi = lds_read_tr16_at(trv[j / 4][1] + off);
-        vop[j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        if (j < 4 * NDB) {
+          const uint32_t off = ST * STAGE_B + 16 * (j % 4) * CPR * 16;
+          const u32x2 lo = lds_read_tr16_at(trv[j / 4][0] + off);
+          const u32x2 hi = lds_read_tr16_at(trv[j / 4][1] + off);
+          vop[j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        } else if (((j - 4 * NDB) & 1) == 0) {
+          // One tail operand per key block, shared by its two row halves.
+          const uint32_t off = ST * STAGE_B + 32 * ((j - 4 * NDB) >> 1) * CPR * 16;
+          const u32x2 lo = lds_read_tr16_at(trt + off);
+          const u32x2 hi = lds_read_tr16_at(trt + off + 16 * CPR * 16);
+          vop[j] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
       };
       f32x16 s[QB][2];
 #pragma unroll
@@ -346,6 +379,13 @@ __global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? (DT == 96 ? 3 : 2) : 1)
             l_i[qb] *= alpha;
 #pragma unroll
             for (int db = 0; db < NDB; ++db) oacc[qb][db] *= alpha;
+            if constexpr (TAIL) {
+              // Tail half hf holds rows 16 hf + l % 16: their alphas.
+              const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(alpha),
+                                                               __float_as_uint(alpha), false, false);
+              otail[qb][0] *= __uint_as_float(sw[0]);
+              otail[qb][1] *= __uint_as_float(sw[1]);
+            }
             m_i[qb] = grow ? mx : m_i[qb];
           }
         }
@@ -373,9 +413,41 @@ __global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? (DT == 96 ? 3 : 2) : 1)
       __builtin_amdgcn_s_setprio(1);
       static_for<0, NPV>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
+        if constexpr (j < 4 * NDB) {
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-          oacc[qb][j / 4] = Elem<T>::mfma(vop[j], pk[qb][j % 4], oacc[qb][j / 4]);
+          for (int qb = 0; qb < QB; ++qb)
+            oacc[qb][j / 4] = Elem<T>::mfma(vop[j], pk[qb][j % 4], oacc[qb][j / 4]);
+        } else {
+          constexpr int u = j - 4 * NDB, kb = u >> 1, hf = u & 1;
+          if constexpr (hf == 0) {
+            // The B operand of a 16x16x32 product for 16 query rows: lane
+            // (n = l % 16, g4 = l / 16) holds row 16 hf + n at 8 keys. Block
+            // kb's P^T has row l % 32 in lane l, with keys 8 (r / 4) + 4 h32
+            // + r % 4 in register r; packing registers {0-3, 8-11} as X and
+            // {4-7, 12-15} as Y, v_permlane16_swap(X, Y) (odd 16-lane groups
+            // of X <-> even groups of Y) leaves rows 0-15 in X and rows 16-31
+            // in Y, with the key slots the tail A operand reads. The PV
+            // products of the 32-wide blocks have consumed pk by now.
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+              for (int w = 0; w < 2; ++w)
+#pragma unroll
+                for (int hs = 0; hs < 2; ++hs) {
+                  const auto sw = __builtin_amdgcn_permlane16_swap(
+                      pk[qb][2 * kb + hs][w], pk[qb][2 * kb + hs][w + 2], false, false);
+                  pk[qb][2 * kb + hs][w] = sw[0];
+                  pk[qb][2 * kb + hs][w + 2] = sw[1];
+                }
+          }
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) {
+            const u32x4 bop = hf == 0
+                ? u32x4{pk[qb][2 * kb][0], pk[qb][2 * kb][1], pk[qb][2 * kb + 1][0], pk[qb][2 * kb + 1][1]}
+                : u32x4{pk[qb][2 * kb][2], pk[qb][2 * kb][3], pk[qb][2 * kb + 1][2], pk[qb][2 * kb + 1][3]};
+            otail[qb][hf] = Elem<T>::mfma16(vop[j - hf], bop, otail[qb][hf]);
+          }
+        }
         if constexpr (j + LA < NPV) read_v(j + LA);
         __builtin_amdgcn_sched_barrier(0);
       });
@@ -497,6 +569,24 @@ __global__ __launch_bounds__(256, ((QB == 1 && !SPLIT) ? (DT == 96 ? 3 : 2) : 1)
       if (h32 == 0) {
         p.lse[((int64_t)b * p.Hq + h) * p.Sq + qrow] =
             lt > 0.f ? (m_i[qb] + fast_log2(lt)) * kLn2 : kNegInf;
+      }
+    }
+    if constexpr (TAIL) {
+      // Tail half hf: lane l holds head dims 64 + 4 (l / 16) .. + 3 of row
+      // 16 hf + l % 16; the rows' 1 / l come over by the same lane swap.
+      const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(inv), __float_as_uint(inv),
+                                                       false, false);
+      const int d = 64 + 4 * (lane >> 4);
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int row = wq0 + qb * 32 + 16 * hf + (lane & 15);
+        const float iv = __uint_as_float(sw[hf]);
+        if (row < p.Sq && d < p.D) {
+          u32x2 w;
+          w[0] = pack2<T>(otail[qb][hf][0] * iv, otail[qb][hf][1] * iv);
+          w[1] = pack2<T>(otail[qb][hf][2] * iv, otail[qb][hf][3] * iv);
+          *reinterpret_cast<u32x2*>(p.o + b * p.o_sb + h * p.o_sh + row * p.o_ss + d) = w;
+        }
       }
     }
   }
