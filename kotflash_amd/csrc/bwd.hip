@@ -211,7 +211,12 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void dq_kernel(const BwdParams 
   constexpr int CPR = DT / 8;
   constexpr int NKS = KS;
   static_assert(KS * 16 <= DT && KS * 16 > DT - 32, "KS covers the tile's head_dim");
-  constexpr int NDB = DT / 32;
+  // Head dims up to 80 in the 96-wide tile (TAIL, tiled form only): dQ^T
+  // columns 0-63 in two 32-wide blocks and 64-79 as a 16-wide tail of
+  // v_mfma_f32_16x16x32 products, as in the forward, so the dQ product runs
+  // 80 columns instead of 96.
+  constexpr bool TAIL = DT == 96 && KS == 5 && !SPLIT;
+  constexpr int NDB = TAIL ? 2 : DT / 32;
   constexpr int TB = BN * DT * 2;       // bytes of one K (or V) tile
   constexpr int STAGE_B = 2 * TB;       // K | V
   constexpr int NST = (SPLIT && DT > 64) ? 1 : 2;  // ring stages
@@ -299,6 +304,9 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void dq_kernel(const BwdParams 
   f32x16 dq[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) dq[db] = zero16();
+  // TAIL: dQ^T head dims 64-79 of rows 16 hf + l % 16 (lane l, register r:
+  // head dim 64 + 4 (l / 16) + r).
+  f32x4 dqt[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 
   const int nkeys = CAUSAL ? min(p.Sk, q0 + BM) : p.Sk;
   const int ntiles = cdiv(nkeys, BN);
@@ -348,7 +356,7 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void dq_kernel(const BwdParams 
   // lo / hi rows 4 h + p / 4 (+ 8) of each 16-key half at head-dim block db.
   // Other stages, the V tile, key blocks and key halves are whole multiples
   // of 16 rows away, which keep the swizzle key, so they are immediates.
-  uint32_t rd[NKS], tr[NDB][2];
+  uint32_t rd[NKS], tr[NDB][2], trt = 0;
 #pragma unroll
   for (int ks = 0; ks < NKS; ++ks) rd[ks] = lds0 + (uint32_t)Tile::chunk(l32, 2 * ks + h32) * 16u;
   {
@@ -361,6 +369,14 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void dq_kernel(const BwdParams 
         const int col = 32 * db + 16 * g + 4 * (pl & 3);
         tr[db][hi] = lds0 + (uint32_t)Tile::elem(r, col) * 2u;
       }
+    // TAIL: the A operand K^T[64 + i][keys] of a 32-key block for lane
+    // (i = l % 16, g4 = l / 16), keys c4 + t and c4 + 16 + t - 4 with
+    // c4 = 8 (g4 & 1) + 4 (g4 >> 1): the forward's tail operand, on K.
+    if constexpr (TAIL) {
+      const int g4 = lane >> 4;
+      const int r = 8 * (g4 & 1) + 4 * (g4 >> 1) + (pl >> 2);
+      trt = lds0 + (uint32_t)Tile::elem(r, 64 + 4 * (pl & 3)) * 2u;
+    }
   }
 
   if (nl > 0) tile_load(tile_of(0), 0);
@@ -389,7 +405,9 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void dq_kernel(const BwdParams 
       // fences keep that order, otherwise the reads trail by one slot and
       // every MFMA waits for its operand.
       constexpr int NSD = 2 * NKS;
-      constexpr int NDQ = 2 * NDB;
+      // dQ slots: 2 NDB 32x32x16 products, then with TAIL two 16x16x32
+      // products (row halves) over the whole 32-key block.
+      constexpr int NDQ = 2 * NDB + (TAIL ? 2 : 0);
       // Operand read-ahead in slots: 5 for the 128-wide tile, the measured
       // optimum at config 3 (A/B in one process, fp16 -3.9%, bf16 -4.1%
       // against 4; 3 is level, 6 slower by 5%, 8 by 17%). At 5 the register
@@ -403,11 +421,16 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void dq_kernel(const BwdParams 
         if (m < NSD) {
           const uint32_t off = ST * STAGE_B + ((m & 1) ? TB : 0) + kb * 32 * CPR * 16;
           op[m] = *(const KF_LDS u32x4*)(uintptr_t)(rd[m >> 1] + off);
-        } else {
+        } else if (m - NSD < 2 * NDB) {
           const int j = m - NSD;
           const uint32_t off = ST * STAGE_B + (32 * kb + 16 * (j & 1)) * CPR * 16;
           const u32x2 lo = lds_read_tr16_at(tr[j >> 1][0] + off);
           const u32x2 hi = lds_read_tr16_at(tr[j >> 1][1] + off);
+          op[m] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        } else if (m - NSD == 2 * NDB) {
+          const uint32_t off = ST * STAGE_B + 32 * kb * CPR * 16;
+          const u32x2 lo = lds_read_tr16_at(trt + off);
+          const u32x2 hi = lds_read_tr16_at(trt + off + 16 * CPR * 16);
           op[m] = u32x4{lo[0], lo[1], hi[0], hi[1]};
         }
       };
@@ -453,12 +476,31 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void dq_kernel(const BwdParams 
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) dp[r] = fast_exp2(s[r]) * dp[r];
-      const u32x4 ds0 = pack8<T>(dp, 0), ds1 = pack8<T>(dp, 8);
+      u32x4 ds0 = pack8<T>(dp, 0), ds1 = pack8<T>(dp, 8);
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(1);
       static_for<0, NDQ>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
-        dq[j >> 1] = Elem<T>::mfma(op[NSD + j], (j & 1) ? ds1 : ds0, dq[j >> 1]);
+        if constexpr (j < 2 * NDB) {
+          dq[j >> 1] = Elem<T>::mfma(op[NSD + j], (j & 1) ? ds1 : ds0, dq[j >> 1]);
+        } else {
+          constexpr int hf = j - 2 * NDB;
+          if constexpr (hf == 0) {
+            // dS^T in the 16x16x32 B layout, by the forward's lane swap:
+            // rows 0-15 in {ds0[0], ds0[1], ds1[0], ds1[1]}, rows 16-31 in
+            // the other halves (the 32-wide dQ products have consumed them).
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+              const auto a = __builtin_amdgcn_permlane16_swap(ds0[w], ds0[w + 2], false, false);
+              const auto c = __builtin_amdgcn_permlane16_swap(ds1[w], ds1[w + 2], false, false);
+              ds0[w] = a[0]; ds0[w + 2] = a[1];
+              ds1[w] = c[0]; ds1[w + 2] = c[1];
+            }
+          }
+          const u32x4 bop = hf == 0 ? u32x4{ds0[0], ds0[1], ds1[0], ds1[1]}
+                                    : u32x4{ds0[2], ds0[3], ds1[2], ds1[3]};
+          dqt[hf] = Elem<T>::mfma16(op[NSD + 2 * NDB], bop, dqt[hf]);
+        }
         if constexpr (NSD + j + LA < NSD + NDQ) read_op(NSD + j + LA);
         __builtin_amdgcn_sched_barrier(0);
       });
@@ -541,6 +583,21 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void dq_kernel(const BwdParams 
           w[1] = pack2<T>(dq[db][4 * g4 + 2] * p.scale, dq[db][4 * g4 + 3] * p.scale);
           *reinterpret_cast<u32x2*>(Dq + d) = w;
         }
+      }
+    }
+  }
+  if constexpr (TAIL) {
+    // Tail half hf: lane l holds head dims 64 + 4 (l / 16) .. + 3 of row
+    // wq0 + 16 hf + l % 16.
+    const int d = 64 + 4 * (lane >> 4);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int row = wq0 + 16 * hf + (lane & 15);
+      if (row < p.Sq && d < p.D) {
+        u32x2 w;
+        w[0] = pack2<T>(dqt[hf][0] * p.scale, dqt[hf][1] * p.scale);
+        w[1] = pack2<T>(dqt[hf][2] * p.scale, dqt[hf][3] * p.scale);
+        *reinterpret_cast<u32x2*>(p.dq + b * p.dq_sb + h * p.dq_sh + row * p.dq_ss + d) = w;
       }
     }
   }
