@@ -468,10 +468,23 @@ __global__ __launch_bounds__(256, SPLIT ? 1 : 2) void dq_kernel(const BwdParams 
       if (need_mask) {
         // Key kb0 + c is visible iff c < lim.
         const int lim = CAUSAL ? min(p.Sk - kb0, qrow - kb0 + 1) : p.Sk - kb0;
+        if constexpr (CAUSAL || DT != 128) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int c = 8 * (r >> 2) + 4 * h32 + (r & 3);
-          s[r] = c < lim ? s[r] : kNegInf;
+          for (int r = 0; r < 16; ++r) {
+            const int c = 8 * (r >> 2) + 4 * h32 + (r & 3);
+            s[r] = c < lim ? s[r] : kNegInf;
+          }
+        } else {
+          // Written as (c - 4 h32) < (lim - 4 h32), every comparison is a
+          // compile-time constant against one per-lane value; comparing the
+          // per-register key offsets themselves, the compiler keeps all 16
+          // in registers across the tile loop, and the non-causal 128-wide
+          // kernel then spilled inside it (this form: dQ -15% at B=4 H=12
+          // S=2048 D=128; the causal kernels ran 0.7% and the non-causal
+          // 96-wide ones 0.4-1% slower with it, so they keep the direct form).
+          const int lh = lim - 4 * h32;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[r] = 8 * (r >> 2) + (r & 3) < lh ? s[r] : kNegInf;
         }
       }
 #pragma unroll
