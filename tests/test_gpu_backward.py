@@ -100,6 +100,28 @@ def test_backward_edge_shapes(shape):
     _check_grads(q, k, v, do, causal, F16, f"{shape}")
 
 
+@pytest.mark.parametrize("shape", [
+    (2, 8, 2, 1100, 1100, 128, True),  # tiled dQ, stream-K dK/dV with shared tiles
+    (1, 6, 6, 700, 700, 96, False),    # 96-wide tile, non-causal MHA
+    (1, 4, 2, 200, 300, 64, False),    # split dQ form (short problem), Sk > Sq
+])
+def test_backward_reads_strided_views_in_place(shape):
+    """q/k/v and dO as [B, S, H, D] storage viewed as [B, H, S, D], the layout
+    a model's projections produce: the kernels read them through their
+    strides (no copy is made) and must match fp32 autograd."""
+    from kotflash_amd.kernels._layout import prepare
+
+    b, hq, hkv, sq, sk, d, causal = shape
+    print(f"strided backward {shape}", flush=True)
+    q = seeded((b, sq, hq, d), 85, dtype=F16).transpose(1, 2)
+    k = seeded((b, sk, hkv, d), 86, dtype=F16).transpose(1, 2)
+    v = seeded((b, sk, hkv, d), 87, dtype=F16).transpose(1, 2)
+    do = seeded((b, sq, hq, d), 88, dtype=F16).transpose(1, 2)
+    for t in (q, k, v, do):
+        assert not t.is_contiguous() and prepare(t, d).data_ptr() == t.data_ptr()
+    _check_grads(q, k, v, do, causal, F16, f"strided {shape}")
+
+
 @pytest.mark.parametrize("dtype", [F16, BF16])
 def test_config3_forward_backward(dtype):
     """B=2, Hq=16, Hkv=4, S=4096, D=128, causal,
