@@ -36,6 +36,17 @@ HIP_FLAGS = [
 ]
 
 
+# Per-file additions. bwd.hip takes the VGPR form of the MFMA builtins: its
+# S/dP products then write VGPRs, where the softmax reads them, while the dK/dV
+# products, written as inline assembly, keep their accumulators in
+# accumulation registers (dkdv_mfma_acc in bwd.hip). Measured on MI355X with
+# bit-identical outputs: dK/dV -1.4% (config 3) to -4.3% (config 4, D = 72),
+# split-form dQ -4 to -7%.
+FILE_FLAGS = {
+    "bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and Path(cand).exists():
@@ -49,7 +60,7 @@ def sources() -> list[Path]:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -666,6 +666,28 @@ struct DkdvSoftPlan {
 //   P  = exp2(scale log2e S - LSE log2e),  dS = P (dP - delta)
 //   dV^T += dO^T P,  dK^T += Q^T dS      (A = transposed LDS reads, B = P / dS
 //                                         straight from the S / dP registers)
+// dV^T / dK^T accumulation, acc += a b on v_mfma_f32_32x32x16, written as
+// inline assembly with the accumulator in accumulation registers ("+a") and
+// the operands in VGPRs. This file is compiled with the VGPR form of the MFMA
+// builtins (-amdgpu-mfma-vgpr-form, set in build.py), so the S and dP
+// products land in VGPRs, where the softmax reads them, instead of in
+// accumulation registers that cost 64 v_accvgpr_read per dK/dV unit; only
+// these products keep the accumulation-register form, which the 256 dK/dV
+// accumulator registers need. The compiler's hazard tracking does not see
+// inside inline assembly, so its wait states are written out: s_nop 1 gives
+// the 2 wait states an MFMA needs after a VALU write of a VGPR it reads (the
+// packed P / dS operands, and the zeroed accumulators at a segment's start,
+// which are hundreds of cycles older still), and the segment flush waits 24
+// wait states before VALU reads the accumulators. Back-to-back products into
+// the same accumulator need none.
+template <typename T>
+__device__ inline void dkdv_mfma_acc(f32x16& acc, u32x4 a, u32x4 b) {
+  if constexpr (std::is_same_v<T, _Float16>)
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  else
+    asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
 template <typename T, int DT, int KS, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const DkdvSplit sp) {
   constexpr int CPR = DT / 8;
@@ -866,6 +888,11 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
       kf[ks] = buf_load16(kr, ok ? (uint32_t)(key * p.k_ss + d) * 2u : kOOB);
       vf[ks] = buf_load16(vr, ok ? (uint32_t)(key * p.v_ss + d) * 2u : kOOB);
     }
+    // The K/V operands live in accumulation registers for the segment (the
+    // S / dP products read their B operand from there): that leaves the
+    // VGPRs to the S and dP accumulators.
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) asm volatile("" : "+a"(kf[ks]), "+a"(vf[ks]));
     wcur = walk_init(b, kvh, qs, nq, ua);
     wdma = wcur;
     const Dma d0 = dma_setup(wdma, 0, true);
@@ -968,9 +995,9 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
           // pk layout: [0] P lo, [1] P hi, [2] dS lo, [3] dS hi
           const int src = (w & 1) ? 2 + (w >> 1) : (w >> 1);
           if ((w & 1) == 0)
-            dv[db] = Elem<T>::mfma(op[m], pk[qb][src], dv[db]);
+            dkdv_mfma_acc<T>(dv[db], op[m], pk[qb][src]);
           else
-            dk[db] = Elem<T>::mfma(op[m], pk[qb][src], dk[db]);
+            dkdv_mfma_acc<T>(dk[db], op[m], pk[qb][src]);
         }
       };
       auto read_stats = [&](int qb) {
@@ -1117,6 +1144,13 @@ __global__ __launch_bounds__(256, 1) void dkdv_kernel(const BwdParams p, const D
       segment_loads();
     }
 
+    // The accumulators were last written by dkdv_mfma_acc, whose results
+    // VALU may read only after the MFMA's passes: 24 wait states cover the
+    // 8-pass 32x32x16 product with margin. The empty operands order the
+    // accumulator reads below after them.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(dk[0]), "+a"(dv[0]));
+#pragma unroll
+    for (int db = 1; db < NDB; ++db) asm volatile("" : "+a"(dk[db]), "+a"(dv[db]));
     // Flush: dK^T / dV^T layout is lane = key, register r = head_dim
     // 32 db + 8 (r/4) + 4 h + r % 4. A tile this workgroup covered alone is
     // final; a shared one goes to this workgroup's partial slot.
