@@ -56,7 +56,7 @@ PEAK_HBM = 8.0e12
 # WRITE_SIZE of the warm dK/dV dispatch of `bench.py --pmc-sample`, each scaled by the
 # factor the same counter reads for a 512 MiB copy / fill in that program
 # (profiles/dkdv_cfg3_hbm_traffic.md). Re-measure when the dK/dV kernel changes.
-DKDV_TRAFFIC_BYTES = 1.529e8
+DKDV_TRAFFIC_BYTES = 1.531e8
 
 
 def log(*a):
