@@ -36,14 +36,20 @@ HIP_FLAGS = [
 ]
 
 
-# Per-file additions. bwd.hip takes the VGPR form of the MFMA builtins: its
-# S/dP products then write VGPRs, where the softmax reads them, while the dK/dV
-# products, written as inline assembly, keep their accumulators in
-# accumulation registers (dkdv_mfma_acc in bwd.hip). Measured on MI355X with
-# bit-identical outputs: dK/dV -1.4% (config 3) to -4.3% (config 4, D = 72),
-# split-form dQ -4 to -7%.
+# Per-file additions: the VGPR form of the MFMA builtins. LLVM chooses the
+# accumulator register class of MFMAs per function; where a kernel also needs
+# accumulation registers (AGPRs) it otherwise writes every MFMA result there,
+# and the softmax then reads S (and dP) back with one v_accvgpr_read per
+# element. With the VGPR form those results land in VGPRs. bwd.hip keeps the
+# dK/dV accumulators in AGPRs through inline-assembly MFMAs (dkdv_mfma_acc).
+# Measured on MI355X, outputs bit-identical: dK/dV -1.4% (config 3) to -4.3%
+# (config 4, D = 72); the split forms of dQ -4 to -7% and of the forward -5%
+# (config 1) to -8%; the D = 96 / 128 decodes -2 to -3%. Kernels that used no
+# AGPRs compile as before.
 FILE_FLAGS = {
     "bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 
