@@ -672,8 +672,8 @@ struct DkdvSoftPlan {
 // builtins (-amdgpu-mfma-vgpr-form, set in build.py), so the S and dP
 // products land in VGPRs, where the softmax reads them, instead of in
 // accumulation registers that cost 64 v_accvgpr_read per dK/dV unit; only
-// these products keep the accumulation-register form, which the 256 dK/dV
-// accumulator registers need. The compiler's hazard tracking does not see
+// these products keep the accumulation-register form, which the 128 dK/dV
+// accumulator registers of the 128-wide tile need. The compiler's hazard tracking does not see
 // inside inline assembly, so its wait states are written out: s_nop 1 gives
 // the 2 wait states an MFMA needs after a VALU write of a VGPR it reads (the
 // packed P / dS operands, and the zeroed accumulators at a segment's start,
